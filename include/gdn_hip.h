@@ -1,0 +1,105 @@
+/*
+ * C ABI of the MI355X (gfx950) gated-delta-rule library, libgdn_hip.so.
+ *
+ * Plain pointers and sizes only; every pointer is device memory unless stated.
+ * All entry points are asynchronous on `stream`, allocate nothing, validate
+ * their arguments on the host before any launch, and return
+ * hipErrorInvalidValue for an unsupported configuration (the reference's
+ * cudaErrorInvalidValue contract, kernels/chunk_delta_cuda.cu:706-708,727),
+ * otherwise the first launch error.  They are reentrant: no global state.
+ *
+ * Tensor layouts (contiguous, row-major) follow kernels/chunk_delta_cuda.h:12-20:
+ *   q, k : bf16 [B, T, HQK, DK]   v-head h reads qk-head h / (HV / HQK)
+ *   v    : bf16 [B, T, HV, DV]
+ *   g    : fp32 [B, T, HV]        log-decay (<= 0), cumulated inside chunks
+ *   beta : fp32 [B, T, HV]
+ *   o    : bf16 [B, T, HV, DV]    (out)
+ *   state: fp32 [B, HV, DK, DV]
+ * q and k are expected L2-normalised by the caller, as in the reference
+ * (kernels/chunk_delta_cuda.h:23-25).  Only DK = DV = 128 and chunk_size = 64
+ * are supported (the reference validates the same single configuration).
+ */
+#ifndef GDN_HIP_H_
+#define GDN_HIP_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_DTYPE_BF16 0
+#define GDN_DTYPE_FP16 1
+#define GDN_DTYPE_FP32 2
+
+/* Workspace bytes for one deltanet_chunk_prefill call (0 for an unsupported
+ * configuration).  Replaces deltanet_prefill_workspace_size,
+ * kernels/chunk_delta_cuda.h:39.  Includes the debug tail, so the same size
+ * serves dump_debug = 0 and 1. */
+size_t deltanet_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int chunk_size);
+
+/* Chunked gated-delta-rule prefill.  Replaces deltanet_chunk_prefill,
+ * kernels/chunk_delta_cuda.h:47-55 (same argument order and meaning; HIP
+ * stream and error types).  initial_state may be NULL (zeros).
+ * dump_debug != 0 additionally writes, past the live workspace, per chunk-head
+ * fp32 T = (I - A)^-1 and A (each [B*NC*HV][64][64]) and the in-chunk cumsum
+ * of g ([B*NC*HV][64]); chunk-head index = (b * NC + chunk) * HV + h. */
+hipError_t deltanet_chunk_prefill(const void* q, const void* k, const void* v, const float* g,
+                                  const float* beta, void* o, const float* initial_state,
+                                  float* final_state, int B, int T, int HV, int HQK, int DK,
+                                  int DV, int chunk_size, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream, int dump_debug);
+
+/* Names of the reference's bf16-wmma o-pass twin (kernels/chunk_delta_cuda_tco.h:39,47);
+ * same implementation and workspace as the two entries above. */
+size_t deltanet_tcop_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int chunk_size);
+hipError_t deltanet_tcop_chunk_prefill(const void* q, const void* k, const void* v,
+                                       const float* g, const float* beta, void* o,
+                                       const float* initial_state, float* final_state, int B,
+                                       int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                       void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream, int dump_debug);
+
+/* Variable-length prefill (no counterpart in the reference kernel: its torch
+ * fallback drops cu_seqlens, transformers modeling_qwen3_5.py:259).
+ * q, k, v, g, beta, o are packed [1, total_tokens, H, D]; cu_seqlens is a
+ * device int32 [num_seqs + 1] with cu_seqlens[0] = 0, non-decreasing,
+ * cu_seqlens[num_seqs] = total_tokens (the caller guarantees this; it is not
+ * read on the host).  initial_state (or NULL) and final_state are
+ * [num_seqs, HV, DK, DV].  Chunks never straddle sequences. */
+size_t deltanet_prefill_varlen_workspace_size(int total_tokens, int num_seqs, int HV, int DK,
+                                              int DV, int chunk_size);
+hipError_t deltanet_chunk_prefill_varlen(const void* q, const void* k, const void* v,
+                                         const float* g, const float* beta, void* o,
+                                         const float* initial_state, float* final_state,
+                                         const int32_t* cu_seqlens, int num_seqs,
+                                         int total_tokens, int HV, int HQK, int DK, int DV,
+                                         int chunk_size, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream,
+                                         int dump_debug);
+
+/* Recurrent step (decode; T >= 1 tokens per sequence), state updated in
+ * place.  Fused native form of the torch token recurrence the reference runs
+ * for decode (transformers modeling_qwen3_5.py:331-380,
+ * torch_recurrent_gated_delta_rule); the reference ships no native decode. */
+hipError_t deltanet_recurrent_step(const void* q, const void* k, const void* v, const float* g,
+                                   const float* beta, void* o, float* state, int B, int T, int HV,
+                                   int HQK, int DK, int DV, hipStream_t stream);
+
+/* Gated RMSNorm y = rmsnorm(x) * w * silu(z) over rows of dv elements.
+ * Replaces kernel::gatedRmsNormForward (export/patches/orin_text_engine/files/
+ * cpp/kernels/gatedRmsNorm/gatedRmsNormKernel.h:17-18), which was fp16-only.
+ * io_dtype (x, z, y): GDN_DTYPE_BF16 or GDN_DTYPE_FP16; w_dtype: io_dtype or
+ * GDN_DTYPE_FP32 (selects transformers' rounding of w * n).
+ * dv in {64, 128, 256, 512}. */
+hipError_t gdn_gated_rmsnorm_forward(const void* x, const void* z, const void* w, void* y,
+                                     int64_t rows, int dv, float eps, int io_dtype, int w_dtype,
+                                     hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_HIP_H_ */

@@ -1,0 +1,276 @@
+"""CPU oracle for the gated-delta-rule (GDN) hot path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product path imports this module:
+only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` use it, and only as the checker (or the timed CPU baseline).
+
+It restates, in plain torch CPU code (fp32 or fp64), the algorithm the
+reference's kernels are gated against.  The defining code is the third-party
+transformers function the reference imports as its parity reference
+(``kernels/harness/parity_test.py:22-27``; a verbatim copy of the same math at
+``kernels/harness/parity_test.py:35-96``), i.e.
+transformers 5.14.1 ``models/qwen3_5/modeling_qwen3_5.py``:
+
+* ``l2norm``                 -> modeling_qwen3_5.py:242-245
+* ``chunk_gated_delta_rule`` -> modeling_qwen3_5.py:249-327 (== parity_test.py:35-96)
+* ``recurrent_gated_delta_rule`` -> modeling_qwen3_5.py:331-380
+* ``gated_rmsnorm``          -> modeling_qwen3_5.py:168-184 (Qwen3_5RMSNormGated)
+* ``gdn_gate``               -> export/patches/orin_text_engine/files/cpp/kernels/
+                                gdnKernels/gdnChunkPrefillSm87.cu:113-125
+* GQA head map               -> kernels/chunk_delta_cuda.h:12-14 (repeat_interleave)
+* tail padding               -> kernels/chunk_delta_cuda.cu:17-19
+
+Layouts follow the reference C ABI (``kernels/chunk_delta_cuda.h:12-20``):
+q, k ``[B, T, HK, DK]``; v ``[B, T, HV, DV]``; g, beta ``[B, T, HV]``;
+state ``[B, HV, DK, DV]``.  Varlen (``cu_seqlens``) is new relative to the
+reference kernel (its torch fallback swallows the argument); the oracle
+defines it as a per-sequence loop over a packed ``[1, sum(T), H, D]`` batch,
+each sequence with its own initial and final state (FLA convention).
+
+Every function here is pinned by tests in ``tests/test_oracle.py``:
+an independent fp64 token recurrence (``recurrence_fp64``), closed forms,
+library routines (``torch.linalg.solve_triangular``, ``F.rms_norm``), the
+installed transformers functions, and invariances (chunk size, resume, GQA,
+padding).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "l2norm",
+    "gdn_gate",
+    "expand_kv_heads",
+    "chunk_gated_delta_rule",
+    "chunk_gated_delta_rule_varlen",
+    "recurrent_gated_delta_rule",
+    "recurrence_fp64",
+    "gated_rmsnorm",
+    "unit_lower_inverse",
+]
+
+
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Row L2 normalisation, eps inside the rsqrt (modeling_qwen3_5.py:242-245)."""
+    return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
+
+
+def gdn_gate(a, b, A_log, dt_bias):
+    """Gate pre-op: g = -exp(A_log) * softplus(a + dt_bias), beta = sigmoid(b).
+
+    Follows gdnChunkPrefillSm87.cu:113-125 and modeling_qwen3_5.py:497-499.
+    Returns fp32 (g, beta) with the [.., HV] layout of ``a`` / ``b``.
+    """
+    a = a.float()
+    b = b.float()
+    g = -torch.exp(A_log.float()) * F.softplus(a + dt_bias.float())
+    return g, torch.sigmoid(b)
+
+
+def expand_kv_heads(x: torch.Tensor, hv: int) -> torch.Tensor:
+    """[B, T, HK, D] -> [B, T, HV, D]: v-head h reads k-head h // (HV // HK)
+    (repeat_interleave semantics, kernels/chunk_delta_cuda.h:12-14)."""
+    hk = x.shape[2]
+    if hk == hv:
+        return x
+    assert hv % hk == 0, "HV must be a multiple of HK"
+    return x.repeat_interleave(hv // hk, dim=2)
+
+
+def unit_lower_inverse(A: torch.Tensor) -> torch.Tensor:
+    """(I - A)^-1 for strictly lower triangular A (batched over leading dims).
+
+    Row-by-row forward substitution, the scheme of modeling_qwen3_5.py:294-297:
+    row i of the inverse is e_i + sum_{j<i} A[i, j] * row_j(inverse), done in
+    place on the strictly lower part before the identity is added.
+    """
+    C = A.shape[-1]
+    X = A.clone()
+    for i in range(1, C):
+        row = X[..., i, :i].clone()
+        sub = X[..., :i, :i].clone()
+        X[..., i, :i] = row + (row.unsqueeze(-1) * sub).sum(-2)
+    return X + torch.eye(C, dtype=A.dtype)
+
+
+def _chunk_core(q, k, v, g, beta, chunk_size, s0, dtype):
+    """Chunked gated delta rule on [B, H, T, D] fp tensors (heads already
+    expanded).  Restates modeling_qwen3_5.py:262-327 term by term:
+
+        c   = cumsum_chunk(g)                 Gamma_rj = exp(c_r - c_j), r >= j
+        A   = -(diag(beta) K K^T o Gamma)     strictly lower
+        T   = (I - A)^-1
+        U   = T diag(beta) V                  W = T diag(beta e^c) K
+        per chunk n:  V_new = U - W S
+                      O     = (Q e^c) S + (Q K^T o Gamma) V_new
+                      S     = e^{c_last} S + (K e^{c_last - c})^T V_new
+    """
+    B, H, T, DK = k.shape
+    DV = v.shape[-1]
+    pad = (chunk_size - T % chunk_size) % chunk_size
+    # zero padding with g = beta = 0 leaves cumsum, decay and state unchanged
+    # (kernels/chunk_delta_cuda.cu:17-19)
+    q = F.pad(q, (0, 0, 0, pad))
+    k = F.pad(k, (0, 0, 0, pad))
+    v = F.pad(v, (0, 0, 0, pad))
+    g = F.pad(g, (0, pad))
+    beta = F.pad(beta, (0, pad))
+    Tp = T + pad
+    n = Tp // chunk_size
+    scale = 1.0 / math.sqrt(DK)
+    q = q * scale
+    qc = q.reshape(B, H, n, chunk_size, DK)
+    kc = k.reshape(B, H, n, chunk_size, DK)
+    vc = v.reshape(B, H, n, chunk_size, DV)
+    bc = beta.reshape(B, H, n, chunk_size)
+    c = g.reshape(B, H, n, chunk_size).cumsum(-1)
+
+    lower_incl = torch.tril(torch.ones(chunk_size, chunk_size, dtype=torch.bool))
+    strict = torch.tril(torch.ones(chunk_size, chunk_size, dtype=torch.bool), -1)
+    diff = c.unsqueeze(-1) - c.unsqueeze(-2)
+    gamma = torch.where(lower_incl, diff, torch.zeros((), dtype=dtype)).exp() * lower_incl
+
+    kb = kc * bc.unsqueeze(-1)
+    A = -(kb @ kc.transpose(-1, -2)) * gamma
+    A = torch.where(strict, A, torch.zeros((), dtype=dtype))
+    Tm = unit_lower_inverse(A)
+    U = Tm @ (vc * bc.unsqueeze(-1))
+    W = Tm @ (kb * c.exp().unsqueeze(-1))
+
+    S = torch.zeros(B, H, DK, DV, dtype=dtype) if s0 is None else s0.to(dtype).clone()
+    out = torch.empty(B, H, n, chunk_size, DV, dtype=dtype)
+    for i in range(n):
+        qi, ki = qc[:, :, i], kc[:, :, i]
+        ci = c[:, :, i]
+        M = (qi @ ki.transpose(-1, -2)) * gamma[:, :, i]
+        v_new = U[:, :, i] - W[:, :, i] @ S
+        out[:, :, i] = (qi * ci.exp().unsqueeze(-1)) @ S + M @ v_new
+        last = ci[..., -1:]
+        kd = ki * (last - ci).exp().unsqueeze(-1)
+        S = S * last.exp().unsqueeze(-1) + kd.transpose(-1, -2) @ v_new
+    out = out.reshape(B, H, Tp, DV)[:, :, :T]
+    return out, S
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, initial_state=None, chunk_size=64,
+                           dtype=torch.float32, use_qk_l2norm=False):
+    """Chunked GDN prefill, reference layout.
+
+    q, k: [B, T, HK, DK]; v: [B, T, HV, DV]; g, beta: [B, T, HV];
+    initial_state: [B, HV, DK, DV] or None (zeros).
+    Returns (o [B, T, HV, DV] in ``dtype``, final_state [B, HV, DK, DV] in ``dtype``).
+    """
+    HV = v.shape[2]
+    q = q.to(dtype)
+    k = k.to(dtype)
+    if use_qk_l2norm:
+        q, k = l2norm(q), l2norm(k)
+    q = expand_kv_heads(q, HV)
+    k = expand_kv_heads(k, HV)
+    tr = lambda x: x.transpose(1, 2).contiguous().to(dtype)  # noqa: E731
+    o, S = _chunk_core(tr(q), tr(k), tr(v), tr(g), tr(beta), chunk_size,
+                       initial_state, dtype)
+    return o.transpose(1, 2).contiguous(), S
+
+
+def chunk_gated_delta_rule_varlen(q, k, v, g, beta, cu_seqlens, initial_state=None,
+                                  chunk_size=64, dtype=torch.float32):
+    """Varlen prefill: packed [1, sum(T), H, D] inputs, ``cu_seqlens`` [N+1],
+    initial_state [N, HV, DK, DV] (or None).  A per-sequence loop of
+    ``chunk_gated_delta_rule``; chunks never straddle sequence boundaries."""
+    cu = [int(x) for x in torch.as_tensor(cu_seqlens).tolist()]
+    N = len(cu) - 1
+    HV, DV = v.shape[2], v.shape[3]
+    DK = k.shape[3]
+    o = torch.zeros(1, cu[-1], HV, DV, dtype=dtype)
+    sf = torch.zeros(N, HV, DK, DV, dtype=dtype)
+    for i in range(N):
+        a, b = cu[i], cu[i + 1]
+        s0 = None if initial_state is None else initial_state[i:i + 1]
+        if b == a:
+            sf[i] = 0 if s0 is None else s0[0].to(dtype)
+            continue
+        oi, si = chunk_gated_delta_rule(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b],
+                                        beta[:, a:b], s0, chunk_size, dtype)
+        o[:, a:b] = oi
+        sf[i] = si[0]
+    return o, sf
+
+
+def recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=None, dtype=torch.float32):
+    """Token recurrence / decode step (modeling_qwen3_5.py:331-380):
+
+        S <- e^{g_t} S;  delta = beta_t (v_t - S^T k_t);  S <- S + k_t delta^T;
+        o_t = (q_t / sqrt(DK))^T S        (o uses the updated state)
+
+    Same layouts as ``chunk_gated_delta_rule``.  Returns (o, final_state).
+    """
+    B, T, HK, DK = q.shape
+    HV, DV = v.shape[2], v.shape[3]
+    q = expand_kv_heads(q.to(dtype), HV) / math.sqrt(DK)
+    k = expand_kv_heads(k.to(dtype), HV)
+    v = v.to(dtype)
+    g = g.to(dtype)
+    beta = beta.to(dtype)
+    S = torch.zeros(B, HV, DK, DV, dtype=dtype) if initial_state is None \
+        else initial_state.to(dtype).clone()
+    o = torch.empty(B, T, HV, DV, dtype=dtype)
+    for t in range(T):
+        S = S * g[:, t].exp()[..., None, None]
+        kv = (S * k[:, t, :, :, None]).sum(-2)
+        delta = (v[:, t] - kv) * beta[:, t, :, None]
+        S = S + k[:, t, :, :, None] * delta[:, :, None, :]
+        o[:, t] = (S * q[:, t, :, :, None]).sum(-2)
+    return o, S
+
+
+def recurrence_fp64(q, k, v, g, beta, s0=None):
+    """Independent brute-force fp64 numpy token recurrence, one head at a time,
+    written directly from the delta-rule update (Yang et al. 2024, "Gated
+    Delta Networks"): S_t = a_t (I - b_t k_t k_t^T) S_{t-1} + b_t k_t v_t^T,
+    o_t = S_t^T q_t / sqrt(DK) with a_t = exp(g_t).
+
+    This form multiplies the projector explicitly, so it shares no code path
+    with the chunked form or with ``recurrent_gated_delta_rule``.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    g = np.asarray(g, dtype=np.float64)
+    beta = np.asarray(beta, dtype=np.float64)
+    B, T, HK, DK = q.shape
+    HV, DV = v.shape[2], v.shape[3]
+    rep = HV // HK
+    o = np.zeros((B, T, HV, DV))
+    S_out = np.zeros((B, HV, DK, DV))
+    eye = np.eye(DK)
+    for b in range(B):
+        for h in range(HV):
+            S = np.zeros((DK, DV)) if s0 is None else np.asarray(s0[b, h], dtype=np.float64).copy()
+            for t in range(T):
+                kt = k[b, t, h // rep]
+                qt = q[b, t, h // rep]
+                P = eye - beta[b, t, h] * np.outer(kt, kt)
+                S = np.exp(g[b, t, h]) * (P @ S) + beta[b, t, h] * np.outer(kt, v[b, t, h])
+                o[b, t, h] = S.T @ qt / math.sqrt(DK)
+            S_out[b, h] = S
+    return o, S_out
+
+
+def gated_rmsnorm(x, z, weight, eps=1e-6):
+    """Qwen3_5RMSNormGated.forward (modeling_qwen3_5.py:175-184) with its
+    dtype steps: normalise in fp32, round to the input dtype, multiply by the
+    weight (in the weight's dtype promotion), multiply by silu(z) in fp32,
+    round to the input dtype.
+    """
+    in_dtype = x.dtype
+    xf = x.to(torch.float32)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    n = (xf * torch.rsqrt(var + eps)).to(in_dtype)
+    h = weight * n
+    h = h * F.silu(z.to(torch.float32))
+    return h.to(in_dtype)

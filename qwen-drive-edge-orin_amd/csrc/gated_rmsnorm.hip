@@ -1,0 +1,165 @@
+// Fused gated RMSNorm for gfx950: y = rmsnorm(x) * w * silu(z).
+//
+// Replaces the TensorRT plugin kernel kern_gated_rmsnorm_fp16
+// (export/patches/orin_text_engine/files/cpp/kernels/gatedRmsNorm/
+// gatedRmsNormKernel.cu:21-64, entry gatedRmsNormForward, .h:17-18) and
+// follows the dtype steps of transformers' Qwen3_5RMSNormGated.forward
+// (modeling_qwen3_5.py:175-184):
+//   n = round_in( x * rsqrt(mean(x^2) + eps) )      (fp32 math)
+//   h = w * n       -- rounded to the input dtype when w has the input dtype,
+//                      kept in fp32 when w is fp32 (torch type promotion)
+//   y = round_in( h * silu(float(z)) )
+//
+// Layout: rows of `dv` contiguous elements.  A row is handled by dv/8 lanes,
+// each moving 16 bytes of x, z and y; the row reduction is a butterfly over
+// those lanes.  Purely HBM-bound: 3 * rows * dv * 2 bytes per call.
+#include "gdn_common.h"
+#include "gdn_hip.h"
+
+#include <math.h>
+
+namespace gdn {
+namespace {
+
+constexpr int kNormThreads = 256;
+
+template <int IO>  // 0 = bf16, 1 = fp16
+__device__ inline float load_elem(uint32_t bits) {
+    if (IO == 0) return bf16_bits_to_f32(bits);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+template <int IO>
+__device__ inline uint32_t store_elem(float f) {
+    if (IO == 0) return f32_to_bf16_bits(f);
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <int IO>
+__device__ inline float round_io(float f) {
+    return load_elem<IO>(store_elem<IO>(f));
+}
+
+// W: 0 = same dtype as the input (bf16/fp16), 2 = fp32
+template <int IO, int W, int LPR>
+__global__ __launch_bounds__(kNormThreads) void gated_rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ z, const void* __restrict__ w,
+    uint16_t* __restrict__ y, int64_t rows, float eps) {
+    constexpr int dv = LPR * 8;
+    const int64_t row = ((int64_t)blockIdx.x * kNormThreads + threadIdx.x) / LPR;
+    const int sub = threadIdx.x % LPR;
+    const bool active = row < rows;
+    const int64_t off = row * dv + sub * 8;
+
+    u32x4 xr = {0u, 0u, 0u, 0u}, zr = {0u, 0u, 0u, 0u};
+    if (active) {
+        xr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + off));
+        zr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(z + off));
+    }
+    const uint32_t xw[4] = {xr[0], xr[1], xr[2], xr[3]};
+    const uint32_t zw[4] = {zr[0], zr[1], zr[2], zr[3]};
+    float xf[8], zf[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        xf[2 * p] = load_elem<IO>(xw[p] & 0xffffu);
+        xf[2 * p + 1] = load_elem<IO>(xw[p] >> 16);
+        zf[2 * p] = load_elem<IO>(zw[p] & 0xffffu);
+        zf[2 * p + 1] = load_elem<IO>(zw[p] >> 16);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(xf[j], xf[j], ss);
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    const float r = 1.0f / sqrtf(ss / (float)dv + eps);
+
+    float wf[8];
+    if (W == 2) {
+        const f32x4* wp = reinterpret_cast<const f32x4*>(static_cast<const float*>(w) + sub * 8);
+        const f32x4 w0 = wp[0], w1 = wp[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wf[j] = w0[j];
+            wf[4 + j] = w1[j];
+        }
+    } else {
+        const u32x4 wr = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w) + sub * 8);
+        const uint32_t ww[4] = {wr[0], wr[1], wr[2], wr[3]};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            wf[2 * p] = load_elem<IO>(ww[p] & 0xffffu);
+            wf[2 * p + 1] = load_elem<IO>(ww[p] >> 16);
+        }
+    }
+    uint32_t out[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * p + h;
+            const float n = round_io<IO>(xf[j] * r);
+            float hv = wf[j] * n;
+            if (W != 2) hv = round_io<IO>(hv);
+            const float sz = zf[j] / (1.0f + expf(-zf[j]));
+            pk |= store_elem<IO>(hv * sz) << (16 * h);
+        }
+        out[p] = pk;
+    }
+    if (active) {
+        const u32x4 o4 = {out[0], out[1], out[2], out[3]};
+        __builtin_nontemporal_store(o4, reinterpret_cast<u32x4*>(y + off));
+    }
+}
+
+template <int IO, int W>
+hipError_t launch_norm(const void* x, const void* z, const void* w, void* y, int64_t rows, int dv,
+                       float eps, hipStream_t stream) {
+    const int lpr = dv / 8;
+    const int64_t rows_per_block = kNormThreads / lpr;
+    const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks), block(kNormThreads);
+    auto xp = static_cast<const uint16_t*>(x);
+    auto zp = static_cast<const uint16_t*>(z);
+    auto yp = static_cast<uint16_t*>(y);
+    switch (lpr) {
+        case 8:
+            hipLaunchKernelGGL((gated_rmsnorm_kernel<IO, W, 8>), grid, block, 0, stream, xp, zp, w, yp, rows, eps);
+            break;
+        case 16:
+            hipLaunchKernelGGL((gated_rmsnorm_kernel<IO, W, 16>), grid, block, 0, stream, xp, zp, w, yp, rows, eps);
+            break;
+        case 32:
+            hipLaunchKernelGGL((gated_rmsnorm_kernel<IO, W, 32>), grid, block, 0, stream, xp, zp, w, yp, rows, eps);
+            break;
+        case 64:
+            hipLaunchKernelGGL((gated_rmsnorm_kernel<IO, W, 64>), grid, block, 0, stream, xp, zp, w, yp, rows, eps);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" hipError_t gdn_gated_rmsnorm_forward(const void* x, const void* z, const void* w,
+                                                void* y, int64_t rows, int dv, float eps,
+                                                int io_dtype, int w_dtype, hipStream_t stream) {
+    if (rows < 0 || !(dv == 64 || dv == 128 || dv == 256 || dv == 512)) return hipErrorInvalidValue;
+    if (!(eps >= 0.f)) return hipErrorInvalidValue;
+    if (io_dtype != GDN_DTYPE_BF16 && io_dtype != GDN_DTYPE_FP16) return hipErrorInvalidValue;
+    if (w_dtype != io_dtype && w_dtype != GDN_DTYPE_FP32) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    if (!x || !z || !w || !y) return hipErrorInvalidValue;
+    if (io_dtype == GDN_DTYPE_BF16)
+        return w_dtype == GDN_DTYPE_FP32
+                   ? launch_norm<0, 2>(x, z, w, y, rows, dv, eps, stream)
+                   : launch_norm<0, 0>(x, z, w, y, rows, dv, eps, stream);
+    return w_dtype == GDN_DTYPE_FP32 ? launch_norm<1, 2>(x, z, w, y, rows, dv, eps, stream)
+                                     : launch_norm<1, 0>(x, z, w, y, rows, dv, eps, stream);
+}

@@ -1,0 +1,78 @@
+// Shared device helpers for the gated-delta-rule kernels (gfx950 / CDNA4).
+//
+// Matrix products run on v_mfma_f32_16x16x32_f16: fp16 operands, fp32
+// accumulation.  bf16 inputs convert to fp16 exactly inside fp16's normal
+// range (|x| in [6.1e-5, 65504]); fp16's 10-bit mantissa keeps the rounding
+// of derived operands (W, V_new, M, decayed K) 8x finer than bf16 would.
+//
+// Operand layout of one 16x16x32 MFMA on a 64-lane wave, lane l, g = l / 16:
+//   A (16 x 32): lane holds row (l % 16), 8 k-values of lane group g
+//   B (32 x 16): lane holds col (l % 16), the same 8 k-values of group g
+//   D (16 x 16): lane holds col (l % 16), rows 4g .. 4g+3
+// Which k a (group, register) slot stands for is a free choice as long as A
+// and B agree.  This library uses one fixed map for every k-block of 32:
+//   k(g, j) = 16 * (j / 4) + 4 * g + (j % 4),   j = 0..7
+// so registers 0..3 of a B operand are rows 4g..4g+3 of one D tile and
+// registers 4..7 the same rows of the next D tile.  A D-layout accumulator
+// therefore feeds the next product as its B operand without any shuffle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kDK = 128;     // key head dim (only validated size)
+constexpr int kDV = 128;     // value head dim
+constexpr int kChunk = 64;   // chunk length
+constexpr int kSlices = 8;   // value-column slices of the state per head
+constexpr int kBV = kDV / kSlices;  // 16 state columns per slice
+
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// k index of (lane group g, register j) inside a 32-wide k-block
+__device__ __forceinline__ constexpr int kmap(int g, int j) {
+    return 16 * (j >> 2) + 4 * g + (j & 3);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ half4 to_half4(f32x4 v) {
+    half4 h;
+    h[0] = (_Float16)v[0];
+    h[1] = (_Float16)v[1];
+    h[2] = (_Float16)v[2];
+    h[3] = (_Float16)v[3];
+    return h;
+}
+
+__device__ __forceinline__ half8 cat8(half4 lo, half4 hi) {
+    half8 r;
+    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+    return r;
+}
+
+__device__ __forceinline__ f32x4 zero4() {
+    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    return z;
+}
+
+}  // namespace gdn

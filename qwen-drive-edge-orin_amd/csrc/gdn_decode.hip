@@ -1,0 +1,132 @@
+// Recurrent gated-delta-rule step (decode, T >= 1) for gfx950.
+//
+// The reference has no native decode; its decode path is the torch token
+// recurrence transformers modeling_qwen3_5.py:331-380
+// (torch_recurrent_gated_delta_rule), per token:
+//   S <- e^{g} S;  kv = S^T k;  delta = beta (v - kv);  S <- S + k delta^T;
+//   o = s S^T q    (o reads the updated state, s = 1/sqrt(DK))
+// which this kernel fuses into one read and one write of S per call:
+//   a = S^T k,  b = S^T q             (one pass over the old state)
+//   delta = beta (v - e^g a)
+//   o = s (e^g b + delta (k . q))     (= s S_new^T q)
+//   S_new = e^g S + k delta^T         (written back in place)
+//
+// One work-group of 256 threads per (batch, v-head) holds the 128x128 fp32
+// state in registers: thread t owns columns 4*(t%32)..+3 of rows
+// (t/32) + 8m, m = 0..15, so every load/store instruction of a wave moves two
+// whole 512-byte rows.  Tokens t > 0 reuse the registers; HBM sees the
+// state exactly once in each direction.
+#include "gdn_common.h"
+#include "gdn_hip.h"
+
+#include <math.h>
+
+namespace gdn {
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kRowsPerThread = kDK / 8;  // 16
+
+__global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* __restrict__ g,
+    const float* __restrict__ beta, uint16_t* __restrict__ o, float* __restrict__ state, int T,
+    int HV, int HK, float scale) {
+    __shared__ float qs[kDK], ks[kDK];
+    __shared__ f32x4 part[4][2][32];  // [wave][a|b][column block]
+    __shared__ float kq;
+
+    const int tid = threadIdx.x;
+    const int cb = tid & 31;   // column block: columns 4cb .. 4cb+3
+    const int rg = tid >> 5;   // row group: rows rg + 8m
+    const int wave = tid >> 6;
+    const int bh = blockIdx.x;  // b * HV + hv
+    const int b = bh / HV, hv = bh - b * HV;
+    const int hk = hv / (HV / HK);
+
+    float* S = state + (size_t)bh * kDK * kDV;
+    f32x4 s[kRowsPerThread];
+#pragma unroll
+    for (int m = 0; m < kRowsPerThread; ++m)
+        s[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + (rg + 8 * m) * kDV) + cb);
+
+    for (int t = 0; t < T; ++t) {
+        const size_t tk = ((size_t)b * T + t);
+        if (tid < kDK) {
+            qs[tid] = bf16_bits_to_f32(q[(tk * HK + hk) * kDK + tid]);
+        } else {
+            ks[tid - kDK] = bf16_bits_to_f32(k[(tk * HK + hk) * kDK + tid - kDK]);
+        }
+        const float gt = g[tk * HV + hv];
+        const float bt = beta[tk * HV + hv];
+        __syncthreads();
+        if (wave == 0) {
+            float p = qs[tid] * ks[tid] + qs[tid + 64] * ks[tid + 64];
+            for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off, 64);
+            if (tid == 0) kq = p;
+        }
+        // partial a = S^T k, b = S^T q over this thread's rows
+        f32x4 pa = zero4(), pb = zero4();
+#pragma unroll
+        for (int m = 0; m < kRowsPerThread; ++m) {
+            const int r = rg + 8 * m;
+            pa += s[m] * ks[r];
+            pb += s[m] * qs[r];
+        }
+        // lanes l and l+32 of a wave share the column block
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pa[i] += __shfl_xor(pa[i], 32, 64);
+            pb[i] += __shfl_xor(pb[i], 32, 64);
+        }
+        if ((tid & 63) < 32) {
+            part[wave][0][cb] = pa;
+            part[wave][1][cb] = pb;
+        }
+        __syncthreads();
+        f32x4 a = part[0][0][cb] + part[1][0][cb] + part[2][0][cb] + part[3][0][cb];
+        f32x4 bq = part[0][1][cb] + part[1][1][cb] + part[2][1][cb] + part[3][1][cb];
+        const float decay = expf(gt);
+        const uint2 vraw = *reinterpret_cast<const uint2*>(v + (tk * HV + hv) * kDV + 4 * cb);
+        f32x4 vv;
+        vv[0] = bf16_bits_to_f32(vraw.x & 0xffffu);
+        vv[1] = bf16_bits_to_f32(vraw.x >> 16);
+        vv[2] = bf16_bits_to_f32(vraw.y & 0xffffu);
+        vv[3] = bf16_bits_to_f32(vraw.y >> 16);
+        const f32x4 delta = (vv - a * decay) * bt;
+        if (rg == 0) {
+            const f32x4 ov = (bq * decay + delta * kq) * scale;
+            uint2 packed;
+            packed.x = (uint32_t)f32_to_bf16_bits(ov[0]) | ((uint32_t)f32_to_bf16_bits(ov[1]) << 16);
+            packed.y = (uint32_t)f32_to_bf16_bits(ov[2]) | ((uint32_t)f32_to_bf16_bits(ov[3]) << 16);
+            *reinterpret_cast<uint2*>(o + (tk * HV + hv) * kDV + 4 * cb) = packed;
+        }
+#pragma unroll
+        for (int m = 0; m < kRowsPerThread; ++m) s[m] = s[m] * decay + delta * ks[rg + 8 * m];
+        __syncthreads();  // qs/ks/part are rewritten by the next token
+    }
+#pragma unroll
+    for (int m = 0; m < kRowsPerThread; ++m)
+        __builtin_nontemporal_store(s[m], reinterpret_cast<f32x4*>(S + (rg + 8 * m) * kDV) + cb);
+}
+
+}  // namespace
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" hipError_t deltanet_recurrent_step(const void* q, const void* k, const void* v,
+                                              const float* g, const float* beta, void* o,
+                                              float* state, int B, int T, int HV, int HQK,
+                                              int DK, int DV, hipStream_t stream) {
+    if (DK != kDK || DV != kDV || B <= 0 || T < 0 || HV <= 0 || HQK <= 0 || HV % HQK != 0)
+        return hipErrorInvalidValue;
+    if (!state) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    hipLaunchKernelGGL(gdn_recurrent_kernel, dim3((unsigned)(B * HV)), dim3(kDecThreads), 0, stream,
+                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                       static_cast<const uint16_t*>(v), g, beta, static_cast<uint16_t*>(o), state,
+                       T, HV, HQK, 1.0f / sqrtf((float)kDK));
+    return hipGetLastError();
+}

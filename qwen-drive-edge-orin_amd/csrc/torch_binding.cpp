@@ -1,0 +1,231 @@
+// Torch extension `deltanet_chunk_hip`: the drop-in for the reference's
+// pybind modules deltanet_chunk_cuda / deltanet_chunk_cuda_tco
+// (kernels/torch_binding.cpp:113-131, kernels/torch_binding_tco.cpp).
+//
+// Same op names, positional order (q, k, v, g, beta, s0) and checks
+// (kernels/torch_binding.cpp:28-30,94-101); errors surface as RuntimeError
+// through TORCH_CHECK.  Every op allocates its outputs and workspace through
+// the caching allocator on the current stream and calls the C ABI of
+// libgdn_hip.so (include/gdn_hip.h) with raw pointers; no torch types cross
+// that boundary.  New relative to the reference: a trailing keyword
+// `cu_seqlens` (varlen prefill), `recurrent_step` (decode) and
+// `gated_rmsnorm`.
+#include <torch/extension.h>
+
+// ROCm torch reports HIP devices as DeviceType::CUDA; the *MasqueradingAsCUDA
+// guard and stream accessors are the ones that accept those devices.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <optional>
+#include <vector>
+
+#include "gdn_hip.h"
+
+namespace {
+
+constexpr int kChunk = 64;
+
+hipStream_t current_stream() { return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
+
+void check_hip(hipError_t err, const char* what) {
+    TORCH_CHECK(err == hipSuccess, what, " failed: ", hipGetErrorString(err));
+}
+
+std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor& k,
+                                           const at::Tensor& v, const at::Tensor& g,
+                                           const at::Tensor& beta,
+                                           const std::optional<at::Tensor>& s0,
+                                           const std::optional<at::Tensor>& cu_seqlens,
+                                           bool debug) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda(),
+                "all inputs must be CUDA tensors");
+    TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
+                    v.scalar_type() == at::kBFloat16,
+                "q/k/v must be bf16");
+    TORCH_CHECK(g.scalar_type() == at::kFloat && beta.scalar_type() == at::kFloat,
+                "g/beta must be fp32");
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && g.dim() == 3 && beta.dim() == 3,
+                "bad ranks");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+
+    auto qc = q.contiguous();
+    auto kc = k.contiguous();
+    auto vc = v.contiguous();
+    auto gc = g.contiguous();
+    auto bc = beta.contiguous();
+    const int64_t B = qc.size(0), T = qc.size(1), HQK = qc.size(2), DK = qc.size(3);
+    const int64_t HV = vc.size(2), DV = vc.size(3);
+    TORCH_CHECK(kc.sizes() == qc.sizes(), "q/k shape mismatch");
+    TORCH_CHECK(vc.size(0) == B && vc.size(1) == T && gc.size(0) == B && gc.size(1) == T &&
+                    bc.size(0) == B && bc.size(1) == T,
+                "batch/time mismatch");
+    TORCH_CHECK(kc.size(2) == HQK && gc.size(2) == HV && bc.size(2) == HV, "head-count mismatch");
+    TORCH_CHECK(HV % HQK == 0, "HV must be a multiple of HQK");
+    TORCH_CHECK(DK == 128 && DV == 128, "only DK = DV = 128 is supported");
+
+    int64_t N = B;
+    at::Tensor cu32;
+    if (cu_seqlens.has_value()) {
+        TORCH_CHECK(cu_seqlens->is_cuda() && cu_seqlens->dim() == 1 && cu_seqlens->numel() >= 2,
+                    "cu_seqlens must be a 1-D CUDA tensor [N+1]");
+        TORCH_CHECK(cu_seqlens->scalar_type() == at::kInt || cu_seqlens->scalar_type() == at::kLong,
+                    "cu_seqlens must be int32 or int64");
+        TORCH_CHECK(B == 1, "cu_seqlens requires packed inputs with batch size 1");
+        cu32 = cu_seqlens->to(at::kInt).contiguous();
+        N = cu32.numel() - 1;
+    }
+
+    auto o = at::empty_like(vc);
+    auto sf = at::empty({N, HV, DK, DV}, vc.options().dtype(at::kFloat));
+    const float* s0p = nullptr;
+    at::Tensor s0c;
+    if (s0.has_value()) {
+        TORCH_CHECK(s0->is_cuda(), "s0 must be a CUDA tensor");
+        s0c = s0->to(at::kFloat).contiguous();
+        TORCH_CHECK(s0c.dim() == 4 && s0c.size(0) == N && s0c.size(1) == HV && s0c.size(2) == DK &&
+                        s0c.size(3) == DV,
+                    "s0 must be [N, HV, DK, DV]");
+        s0p = s0c.data_ptr<float>();
+    }
+
+    const size_t ws_bytes =
+        cu_seqlens.has_value()
+            ? deltanet_prefill_varlen_workspace_size((int)T, (int)N, (int)HV, (int)DK, (int)DV, kChunk)
+            : deltanet_prefill_workspace_size((int)B, (int)T, (int)HV, (int)DK, (int)DV, kChunk);
+    TORCH_CHECK(ws_bytes > 0, "unsupported prefill configuration");
+    auto ws = at::empty({(int64_t)ws_bytes}, vc.options().dtype(at::kByte));
+
+    hipError_t err;
+    if (cu_seqlens.has_value()) {
+        err = deltanet_chunk_prefill_varlen(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr<float>(), bc.data_ptr<float>(),
+            o.data_ptr(), s0p, sf.data_ptr<float>(), cu32.data_ptr<int32_t>(), (int)N, (int)T,
+            (int)HV, (int)HQK, (int)DK, (int)DV, kChunk, ws.data_ptr(), ws_bytes,
+            current_stream(), debug ? 1 : 0);
+    } else {
+        err = deltanet_chunk_prefill(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                     gc.data_ptr<float>(), bc.data_ptr<float>(), o.data_ptr(), s0p,
+                                     sf.data_ptr<float>(), (int)B, (int)T, (int)HV, (int)HQK,
+                                     (int)DK, (int)DV, kChunk, ws.data_ptr(), ws_bytes,
+                                     current_stream(), debug ? 1 : 0);
+    }
+    check_hip(err, "deltanet_chunk_prefill");
+
+    std::vector<at::Tensor> out{o, sf};
+    if (debug) {
+        // debug tail: [T | A | cumsum(g)] per chunk-head, the last three
+        // regions of the workspace (each 256-byte aligned, see gdn_prefill.hip)
+        const int64_t nc = cu_seqlens.has_value() ? (T + (int64_t)(kChunk - 1) * N) / kChunk
+                                                  : B * ((T + kChunk - 1) / kChunk);
+        const int64_t nch = nc * HV;
+        auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
+        const int64_t tail = al(nch * kChunk * kChunk * 4) * 2 + al(nch * kChunk * 4);
+        const int64_t off = (int64_t)ws_bytes - tail;
+        auto wsf = [&](int64_t byte_off, int64_t count) {
+            return ws.narrow(0, byte_off, count * 4).view(at::kFloat);
+        };
+        out.push_back(wsf(off, nch * kChunk * kChunk).view({nc, HV, kChunk, kChunk}));
+        out.push_back(wsf(off + al(nch * kChunk * kChunk * 4), nch * kChunk * kChunk)
+                          .view({nc, HV, kChunk, kChunk}));
+        out.push_back(wsf(off + 2 * al(nch * kChunk * kChunk * 4), nch * kChunk).view({nc, HV, kChunk}));
+    }
+    return out;
+}
+
+}  // namespace
+
+std::vector<at::Tensor> chunk_prefill(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
+                                      at::Tensor beta, std::optional<at::Tensor> s0,
+                                      std::optional<at::Tensor> cu_seqlens) {
+    return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/false);
+}
+
+std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tensor v,
+                                            at::Tensor g, at::Tensor beta,
+                                            std::optional<at::Tensor> s0,
+                                            std::optional<at::Tensor> cu_seqlens) {
+    return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/true);
+}
+
+at::Tensor recurrent_step(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
+                          at::Tensor beta, at::Tensor state) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda() &&
+                    state.is_cuda(),
+                "all inputs must be CUDA tensors");
+    TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
+                    v.scalar_type() == at::kBFloat16,
+                "q/k/v must be bf16");
+    TORCH_CHECK(g.scalar_type() == at::kFloat && beta.scalar_type() == at::kFloat &&
+                    state.scalar_type() == at::kFloat,
+                "g/beta/state must be fp32");
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && g.dim() == 3 && beta.dim() == 3 &&
+                    state.dim() == 4,
+                "bad ranks");
+    TORCH_CHECK(state.is_contiguous(), "state is updated in place and must be contiguous");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto qc = q.contiguous();
+    auto kc = k.contiguous();
+    auto vc = v.contiguous();
+    auto gc = g.contiguous();
+    auto bc = beta.contiguous();
+    const int64_t B = qc.size(0), T = qc.size(1), HQK = qc.size(2), DK = qc.size(3);
+    const int64_t HV = vc.size(2), DV = vc.size(3);
+    TORCH_CHECK(kc.sizes() == qc.sizes(), "q/k shape mismatch");
+    TORCH_CHECK(vc.size(0) == B && vc.size(1) == T && gc.size(0) == B && gc.size(1) == T &&
+                    gc.size(2) == HV && bc.sizes() == gc.sizes(),
+                "batch/time/head mismatch");
+    TORCH_CHECK(HV % HQK == 0, "HV must be a multiple of HQK");
+    TORCH_CHECK(state.size(0) == B && state.size(1) == HV && state.size(2) == DK &&
+                    state.size(3) == DV,
+                "state must be [B, HV, DK, DV]");
+    auto o = at::empty_like(vc);
+    check_hip(deltanet_recurrent_step(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                      gc.data_ptr<float>(), bc.data_ptr<float>(), o.data_ptr(),
+                                      state.data_ptr<float>(), (int)B, (int)T, (int)HV, (int)HQK,
+                                      (int)DK, (int)DV, current_stream()),
+              "deltanet_recurrent_step");
+    return o;
+}
+
+at::Tensor gated_rmsnorm(at::Tensor x, at::Tensor z, at::Tensor weight, double eps) {
+    TORCH_CHECK(x.is_cuda() && z.is_cuda() && weight.is_cuda(), "all inputs must be CUDA tensors");
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf,
+                "x must be bf16 or fp16");
+    TORCH_CHECK(z.scalar_type() == x.scalar_type(), "z must have the dtype of x");
+    TORCH_CHECK(weight.scalar_type() == x.scalar_type() || weight.scalar_type() == at::kFloat,
+                "weight must have the dtype of x or be fp32");
+    TORCH_CHECK(x.sizes() == z.sizes(), "x/z shape mismatch");
+    TORCH_CHECK(x.dim() >= 1 && weight.dim() == 1 && weight.size(0) == x.size(-1),
+                "weight must be [x.size(-1)]");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    auto xc = x.contiguous();
+    auto zc = z.contiguous();
+    auto wc = weight.contiguous();
+    auto y = at::empty_like(xc);
+    const int dv = (int)xc.size(-1);
+    const int64_t rows = dv > 0 ? xc.numel() / dv : 0;
+    const int io = x.scalar_type() == at::kBFloat16 ? GDN_DTYPE_BF16 : GDN_DTYPE_FP16;
+    const int wd = weight.scalar_type() == at::kFloat ? GDN_DTYPE_FP32 : io;
+    check_hip(gdn_gated_rmsnorm_forward(xc.data_ptr(), zc.data_ptr(), wc.data_ptr(), y.data_ptr(),
+                                        rows, dv, (float)eps, io, wd, current_stream()),
+              "gdn_gated_rmsnorm_forward");
+    return y;
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    using namespace pybind11::literals;
+    m.def("chunk_prefill", &chunk_prefill,
+          "chunked gated delta rule prefill (gfx950 HIP); returns [o, final_state]", "q"_a, "k"_a,
+          "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
+          "cu_seqlens"_a = std::nullopt);
+    m.def("chunk_prefill_debug", &chunk_prefill_debug,
+          "same, also returns per-chunk-head T=(I-A)^-1, A and cumsum(g) views", "q"_a, "k"_a,
+          "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
+          "cu_seqlens"_a = std::nullopt);
+    m.def("recurrent_step", &recurrent_step,
+          "recurrent gated delta rule (decode), state updated in place; returns o", "q"_a, "k"_a,
+          "v"_a, "g"_a, "beta"_a, "state"_a);
+    m.def("gated_rmsnorm", &gated_rmsnorm, "y = rmsnorm(x) * weight * silu(z)", "x"_a, "z"_a,
+          "weight"_a, "eps"_a = 1e-6);
+}

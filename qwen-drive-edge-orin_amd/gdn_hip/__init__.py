@@ -1,0 +1,62 @@
+"""gdn_hip: MI355X (gfx950) gated-delta-rule ops.
+
+The compiled pieces live next to this file:
+  libgdn_hip.so            C ABI (include/gdn_hip.h)
+  deltanet_chunk_hip*.so   torch extension over it, the drop-in for the
+                           reference's deltanet_chunk_cuda / _tco modules
+                           (kernels/torch_binding.cpp:113-131)
+
+``load()`` returns the extension module, whose ops are
+
+  chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None) -> [o, final_state]
+  chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
+  recurrent_step(q, k, v, g, beta, state) -> o          (state updated in place)
+  gated_rmsnorm(x, z, weight, eps=1e-6) -> y
+
+There is no fallback: if the extension is not built, ``load()`` raises.
+Build with ``python qwen-drive-edge-orin_amd/build.py``.
+"""
+from __future__ import annotations
+
+import importlib
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libgdn_hip.so"
+EXT_NAME = "deltanet_chunk_hip"
+
+_mod = None
+
+
+def ext_path() -> Path | None:
+    hits = sorted(HERE.glob(f"{EXT_NAME}.cpython*.so"))
+    return hits[0] if hits else None
+
+
+def load():
+    """Import the in-tree torch extension (raises ImportError when missing)."""
+    global _mod
+    if _mod is None:
+        if not LIB_PATH.exists() or ext_path() is None:
+            raise ImportError(
+                f"gdn_hip native code is not built under {HERE}; run "
+                "`python qwen-drive-edge-orin_amd/build.py`")
+        import torch  # noqa: F401  (loads libc10/libtorch the extension links)
+        _mod = importlib.import_module(f"{__name__}.{EXT_NAME}")
+    return _mod
+
+
+def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
+    return load().chunk_prefill(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens)
+
+
+def chunk_prefill_debug(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
+    return load().chunk_prefill_debug(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens)
+
+
+def recurrent_step(q, k, v, g, beta, state):
+    return load().recurrent_step(q, k, v, g, beta, state)
+
+
+def gated_rmsnorm(x, z, weight, eps=1e-6):
+    return load().gated_rmsnorm(x, z, weight, eps)

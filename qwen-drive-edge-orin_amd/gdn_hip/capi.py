@@ -1,0 +1,66 @@
+"""ctypes view of libgdn_hip.so's C ABI (include/gdn_hip.h).
+
+This is the binding a Python caller of the reference's C entry points would
+write; the tests use it to call the boundary directly with raw device
+pointers, and to check that every declared symbol is exported.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import re
+from pathlib import Path
+
+from . import LIB_PATH
+
+HEADER = Path(__file__).resolve().parents[2] / "include" / "gdn_hip.h"
+
+hipError_t = ct.c_int
+hipStream_t = ct.c_void_p
+vp, fp, i32p = ct.c_void_p, ct.c_void_p, ct.c_void_p
+c_int, c_size_t, c_int64, c_float = ct.c_int, ct.c_size_t, ct.c_int64, ct.c_float
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+DTYPE_BF16, DTYPE_FP16, DTYPE_FP32 = 0, 1, 2
+
+_PROTOS = {
+    "deltanet_prefill_workspace_size": (c_size_t, [c_int] * 6),
+    "deltanet_tcop_prefill_workspace_size": (c_size_t, [c_int] * 6),
+    "deltanet_chunk_prefill": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
+                               [vp, c_size_t, hipStream_t, c_int]),
+    "deltanet_tcop_chunk_prefill": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
+                                    [vp, c_size_t, hipStream_t, c_int]),
+    "deltanet_prefill_varlen_workspace_size": (c_size_t, [c_int] * 6),
+    "deltanet_chunk_prefill_varlen": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, i32p] +
+                                      [c_int] * 7 + [vp, c_size_t, hipStream_t, c_int]),
+    "deltanet_recurrent_step": (hipError_t, [vp, vp, vp, fp, fp, vp, fp] + [c_int] * 6 +
+                                [hipStream_t]),
+    "gdn_gated_rmsnorm_forward": (hipError_t, [vp, vp, vp, vp, c_int64, c_int, c_float, c_int,
+                                               c_int, hipStream_t]),
+}
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/gdn_hip.h."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:size_t|hipError_t)\s+(\w+)\s*\(", text, flags=re.M)
+
+
+_lib = None
+
+
+def lib() -> ct.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = ct.CDLL(str(LIB_PATH))
+        for name, (res, args) in _PROTOS.items():
+            f = getattr(_lib, name)
+            f.restype = res
+            f.argtypes = args
+    return _lib
+
+
+def ptr(t) -> int | None:
+    """Raw data pointer of a torch tensor (None for None)."""
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,87 @@
+"""GPU parity of the recurrent decode step and the gated RMSNorm."""
+import pytest
+import torch
+
+import gdn_cases as gc
+from oracle import gdn_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode_check(ops, dev, q, k, v, g, beta, s0, tag):
+    print(f"[decode] {tag} q={tuple(q.shape)} v={tuple(v.shape)}", flush=True)
+    state = s0.to(dev).clone()
+    o = ops.recurrent_step(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), state)
+    torch.cuda.synchronize()
+    o_ref, s_ref = orc.recurrent_gated_delta_rule(q, k, v, g, beta, s0, dtype=torch.float64)
+    mo, ms = gc.parity(o, o_ref), gc.parity(state, s_ref)
+    print(f"    o: {gc.fmt(mo)}\n    S: {gc.fmt(ms)}", flush=True)
+    gc.assert_abs(mo, what=f"{tag} o")
+    gc.assert_abs(ms, what=f"{tag} state")
+    gc.assert_ref_bar(mo, what=f"{tag} o")
+    gc.assert_ref_bar(ms, what=f"{tag} state")
+    return o, state
+
+
+def test_c3_decode(ops, dev):
+    """B64 T1 HV32 HK16 d128, fp32 state updated in place."""
+    _decode_check(ops, dev, *gc.c3_inputs(), tag="c3")
+
+
+@pytest.mark.parametrize("T", [2, 5])
+@pytest.mark.parametrize("hk,hv", [(2, 4), (4, 4)])
+def test_multi_token(ops, dev, T, hk, hv):
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(40 + T + hk, B=3, T=T, HK=hk, HV=hv, s0_scale=0.5)
+    _decode_check(ops, dev, q, k, v, g, beta, s0, tag=f"T{T} hk{hk} hv{hv}")
+
+
+def test_decode_matches_prefill_t1(ops, dev):
+    """A T=1 prefill and a decode step compute the same token."""
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.make_gdn_inputs(9, B=4, T=1, HK=2, HV=4)]
+    o_p, s_p = ops.chunk_prefill(q, k, v, g, beta, s0)
+    st = s0.clone()
+    o_d = ops.recurrent_step(q, k, v, g, beta, st)
+    assert (o_p.float() - o_d.float()).abs().max().item() < 2e-3
+    assert (s_p - st).abs().max().item() < 2e-3
+
+
+def _norm_check(ops, dev, x, z, w, eps, tag):
+    print(f"[rmsnorm] {tag} x={tuple(x.shape)} {x.dtype} w={w.dtype}", flush=True)
+    y = ops.gated_rmsnorm(x.to(dev), z.to(dev), w.to(dev), eps)
+    torch.cuda.synchronize()
+    y_ref = orc.gated_rmsnorm(x, z, w, eps)
+    y = y.cpu()
+    exact = (y == y_ref).float().mean().item()
+    d = (y.float() - y_ref.float()).abs()
+    # The GPU and CPU differ only in fp32 summation order and exp/sqrt last
+    # bits, which can flip one of the three roundings (n, w*n, y).  A flip in
+    # n moves y by ulp(n)|w||silu z|, so bound by one rounding step of each
+    # stage at its own magnitude (2^-8 relative for bf16, 2^-11 for fp16).
+    u = 2 ** -8 if x.dtype == torch.bfloat16 else 2 ** -11
+    xf, zf = x.float(), z.float()
+    n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    stage = (w.float() * n * torch.nn.functional.silu(zf)).abs()
+    bound = 2 * u * (2 * stage + y_ref.float().abs()) + 1e-6
+    print(f"    bitwise={exact * 100:.4f}% max_abs={d.max().item():.3e} "
+          f"cos={gc.row_cos_min(y, y_ref):.8f}", flush=True)
+    assert not torch.isnan(y).any()
+    assert (d <= bound).all(), "more than one rounding step per stage off"
+    assert exact >= 0.999
+    return y
+
+
+def test_c2_gated_rmsnorm(ops, dev):
+    """rows 1141x32, d128, bf16 o/z/w, eps 1e-6 (HF Qwen3_5RMSNormGated rounding)."""
+    _norm_check(ops, dev, *gc.c2_inputs(), tag="c2")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("wdt", ["io", "fp32"])
+@pytest.mark.parametrize("dv", [64, 128, 256, 512])
+def test_rmsnorm_variants(ops, dev, dtype, wdt, dv):
+    gen = torch.Generator().manual_seed(dv)
+    x = torch.randn(37, 3, dv, generator=gen).to(dtype)
+    z = torch.randn(37, 3, dv, generator=gen).to(dtype)
+    w = 1 + 0.1 * torch.randn(dv, generator=gen)
+    w = w.to(dtype) if wdt == "io" else w
+    _norm_check(ops, dev, x, z, w, 1e-6, tag=f"{dtype} w={wdt} dv={dv}")

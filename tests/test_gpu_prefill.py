@@ -1,0 +1,141 @@
+"""GPU parity of the chunked prefill against the CPU oracle.
+
+The oracle runs in fp64 on the same bf16/fp32 input tensors.  Bars:
+max |err| <= 2e-2 on o and on the final state (mean error printed), and the
+reference harness's random-case bar (row-cos >= 0.999, max-rel < 1e-2 with
+denominator floor 0.1; kernels/harness/parity_test.py:188-189).
+"""
+import pytest
+import torch
+
+import gdn_cases as gc
+from oracle import gdn_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_and_check(ops, dev, q, k, v, g, beta, s0, tag, ref_bar=True, cu=None):
+    print(f"[prefill] {tag} q={tuple(q.shape)} v={tuple(v.shape)} s0={'Y' if s0 is not None else 'n'}"
+          f" cu={'Y' if cu is not None else 'n'}", flush=True)
+    args = [t.to(dev) if t is not None else None for t in (q, k, v, g, beta, s0)]
+    if cu is None:
+        o, sf = ops.chunk_prefill(*args)
+        o_ref, s_ref = orc.chunk_gated_delta_rule(q, k, v, g, beta, s0, dtype=torch.float64)
+    else:
+        o, sf = ops.chunk_prefill(*args, cu_seqlens=cu.to(dev))
+        o_ref, s_ref = orc.chunk_gated_delta_rule_varlen(q, k, v, g, beta, cu, s0,
+                                                         dtype=torch.float64)
+    torch.cuda.synchronize()
+    mo, ms = gc.parity(o, o_ref), gc.parity(sf, s_ref)
+    print(f"    o: {gc.fmt(mo)}\n    S: {gc.fmt(ms)}", flush=True)
+    gc.assert_abs(mo, what=f"{tag} o")
+    gc.assert_abs(ms, what=f"{tag} state")
+    if ref_bar:
+        gc.assert_ref_bar(mo, what=f"{tag} o")
+        gc.assert_ref_bar(ms, what=f"{tag} state")
+    return o, sf
+
+
+def test_c4_planner_shape(ops, dev):
+    """B1 T1141 HV32 HK16 d128: ragged 53-row tail chunk, GQA 2:1."""
+    _run_and_check(ops, dev, *gc.c4_inputs(), tag="c4")
+
+
+def test_c5_varlen(ops, dev):
+    """8 sequences of seed-7 lengths (sum 19861), independent initial states."""
+    q, k, v, g, beta, s0, cu = gc.c5_inputs()
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="c5", cu=cu)
+
+
+@pytest.mark.parametrize("T", [1, 2, 17, 63, 64, 65, 127, 128, 200])
+@pytest.mark.parametrize("B", [1, 2])
+def test_small_shapes(ops, dev, T, B):
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(100 + T * 3 + B, B=B, T=T, HK=2, HV=4)
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag=f"T{T}B{B}")
+
+
+@pytest.mark.parametrize("hk,hv", [(4, 4), (1, 4), (2, 8), (3, 6)])
+def test_head_maps(ops, dev, hk, hv):
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(7 + hk * 10 + hv, B=1, T=150, HK=hk, HV=hv,
+                                              with_s0=False)
+    _run_and_check(ops, dev, q, k, v, g, beta, None, tag=f"hk{hk}hv{hv}")
+
+
+@pytest.mark.parametrize("l2_pre", [False, True])
+@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("S", [128, 512, 3200])
+def test_reference_grid(ops, dev, l2_pre, B, S):
+    """The reference harness's random grid (kernels/harness/parity_cuda.py:146-153):
+    H=32 heads (q/k pre-expanded), q/k = randn/8, g = -0.3 rand, beta = rand."""
+    seed = hash((B, S, l2_pre)) % 2 ** 31
+    q, k, v, g, beta, s0 = gc.make_reference_inputs(B, S, seed, l2_pre=l2_pre)
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag=f"grid S{S} B{B} l2={l2_pre}")
+
+
+def test_reference_grid_init_state(ops, dev):
+    """parity_cuda.py:154-156: B=1, S=512 with a random initial state."""
+    q, k, v, g, beta, s0 = gc.make_reference_inputs(1, 512, hash((1, 512, False)) % 2 ** 31,
+                                                     with_init_state=True)
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="grid init")
+
+
+def test_varlen_edges(ops, dev):
+    """Empty, single-token and chunk-boundary lengths in one packed batch."""
+    lens = torch.tensor([0, 1, 63, 64, 65, 0, 130, 5])
+    q, k, v, g, beta, s0, cu = gc.c5_inputs(lens)
+    o, sf = _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="varlen-edges", cu=cu)
+    # empty sequences pass their initial state through unchanged
+    assert torch.equal(sf[0].cpu(), s0[0].float())
+    assert torch.equal(sf[5].cpu(), s0[5].float())
+
+
+def test_varlen_equals_per_sequence_calls(ops, dev):
+    """Size-independent property at the c5 size: the packed call is bitwise the
+    per-sequence fixed-length calls (same chunking, same kernels)."""
+    q, k, v, g, beta, s0, cu = gc.c5_inputs()
+    d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
+    o, sf = ops.chunk_prefill(*d, cu_seqlens=cu.to(dev))
+    for i in range(len(cu) - 1):
+        a, b = int(cu[i]), int(cu[i + 1])
+        oi, si = ops.chunk_prefill(d[0][:, a:b], d[1][:, a:b], d[2][:, a:b], d[3][:, a:b],
+                                   d[4][:, a:b], d[5][i:i + 1])
+        assert torch.equal(oi, o[:, a:b]), f"seq {i} o"
+        assert torch.equal(si[0], sf[i]), f"seq {i} state"
+
+
+def test_gqa_equals_expanded_heads(ops, dev):
+    """HK=16 -> HV=32 sharing is bitwise the explicit repeat_interleave."""
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.c4_inputs()]
+    o1, s1 = ops.chunk_prefill(q, k, v, g, beta, s0)
+    o2, s2 = ops.chunk_prefill(q.repeat_interleave(2, 2), k.repeat_interleave(2, 2), v, g, beta, s0)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_resume_split(ops, dev):
+    """Running [0, 640) then [640, T) from the carried state matches one call
+    (chunk-aligned split, so the chunking is identical: bitwise)."""
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.c4_inputs()]
+    o, sf = ops.chunk_prefill(q, k, v, g, beta, s0)
+    t = 640
+    oa, sa = ops.chunk_prefill(q[:, :t], k[:, :t], v[:, :t], g[:, :t], beta[:, :t], s0)
+    ob, sb = ops.chunk_prefill(q[:, t:], k[:, t:], v[:, t:], g[:, t:], beta[:, t:], sa)
+    assert torch.equal(torch.cat([oa, ob], 1), o) and torch.equal(sb, sf)
+
+
+def test_debug_views(ops, dev):
+    """chunk_prefill_debug's T, A and cumsum(g) views against the oracle's
+    chunk-local quantities (T checked against a triangular solve)."""
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(11, B=1, T=100, HK=2, HV=4)
+    d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
+    o, sf, Tm, A, cg = ops.chunk_prefill_debug(*d)
+    o2, sf2 = ops.chunk_prefill(*d)
+    assert torch.equal(o, o2) and torch.equal(sf, sf2)
+    Tm, A, cg = Tm.cpu().double(), A.cpu().double(), cg.cpu().double()
+    nc = 2
+    assert Tm.shape == (nc, 4, 64, 64) and cg.shape == (nc, 4, 64)
+    # cumsum of g per chunk (padded rows carry the last value)
+    gp = torch.nn.functional.pad(g.double(), (0, 0, 0, 28))[0].reshape(nc, 64, 4).permute(0, 2, 1)
+    assert torch.allclose(cg, gp.cumsum(-1), atol=1e-5)
+    eye = torch.eye(64, dtype=torch.float64)
+    inv = torch.linalg.solve_triangular(eye - A, eye, upper=False, unitriangular=True)
+    assert torch.allclose(Tm, inv, atol=1e-5, rtol=1e-4)
