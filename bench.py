@@ -1,0 +1,342 @@
+"""Benchmark of the gated-delta-rule prefill on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+One step = one chunked gated-delta prefill call (q, k, v, g, beta,
+initial_state -> o, final_state) at the planner shape B=1, T=1141, HV=32,
+HK=16, d=128, bf16 inputs, fp32 state, synthetic seeded data.  Inputs are
+resident in HBM before timing starts; successive steps rotate through enough
+input copies (> 256 MB) that the Infinity Cache cannot serve them, so the
+timed number is the cold one.  The warm (same inputs every step) number and
+the secondary workloads (gated RMSNorm, decode step, varlen prefill) are
+reported in the same JSON line.
+
+Prints ONE JSON line.  `value` is TFLOP/s under the fixed dense FLOP
+convention of 182.95 kFLOP per token per v-head.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "qwen-drive-edge-orin_amd", ROOT / "tests"):
+    sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA, published
+MALL_BYTES = 256 << 20
+
+
+def _bytes(*ts):
+    return sum(t.numel() * t.element_size() for t in ts if t is not None)
+
+
+def time_calls(fn, n_sets, steps, warmup):
+    """HIP-event time of `steps` back-to-back calls fn(i) on the current
+    stream, bracketed by device synchronisation; returns ms per call."""
+    import torch
+
+    for i in range(warmup):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i % n_sets)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def rotation(make, per_set_bytes, dev, min_total=2 * MALL_BYTES, max_sets=64):
+    n = max(2, min(max_sets, -(-min_total // max(per_set_bytes, 1))))
+    base = [t.to(dev) if hasattr(t, "to") else t for t in make()]
+    sets = [base] + [[t.clone() if hasattr(t, "clone") else t for t in base] for _ in range(n - 1)]
+    return sets
+
+
+def bench_prefill(ops, dev, steps, warmup):
+    import torch
+    import gdn_cases as gc
+
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    in_bytes = _bytes(q, k, v, g, beta, s0)
+    sets = rotation(lambda: (q, k, v, g, beta, s0), in_bytes, dev)
+    fn = lambda i: ops.chunk_prefill(*sets[i])  # noqa: E731
+    cold_ms = time_calls(fn, len(sets), steps, warmup)
+    warm_ms = time_calls(lambda i: ops.chunk_prefill(*sets[0]), 1, steps, warmup)
+    T, HV = q.shape[1], v.shape[2]
+    flops = gc.flops_prefill(T, HV)
+    out_bytes = _bytes(v) + _bytes(s0)  # o (bf16, like v) + final state
+    algo_bytes = in_bytes + out_bytes
+    return dict(cold_ms=cold_ms, warm_ms=warm_ms, flops=flops, algo_bytes=algo_bytes,
+                n_sets=len(sets), T=T, HV=HV)
+
+
+def bench_varlen(ops, dev, steps, warmup):
+    import gdn_cases as gc
+
+    q, k, v, g, beta, s0, cu = gc.varlen_inputs()
+    d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
+    cud = cu.to(dev)
+    ms = time_calls(lambda i: ops.chunk_prefill(*d, cu_seqlens=cud), 1, steps, warmup)
+    total = int(cu[-1])
+    flops = gc.flops_prefill(total, v.shape[2])
+    algo = _bytes(q, k, v, g, beta, s0) + _bytes(v) + _bytes(s0)
+    return dict(ms=ms, tflops=flops / ms / 1e9, gbs=algo / ms / 1e6, tokens=total)
+
+
+def bench_decode(ops, dev, steps, warmup):
+    import gdn_cases as gc
+
+    q, k, v, g, beta, s0 = gc.decode_inputs()
+    per = _bytes(q, k, v, g, beta, s0)
+    sets = rotation(lambda: (q, k, v, g, beta, s0), per, dev)
+    ms = time_calls(lambda i: ops.recurrent_step(*sets[i]), len(sets), steps, warmup)
+    algo = per + _bytes(s0) + _bytes(v)  # state read + written, o written
+    return dict(ms=ms, gbs=algo / ms / 1e6, frac=algo / ms / 1e6 / HBM_PEAK_GBS, bytes=algo)
+
+
+def bench_norm(ops, dev, steps, warmup):
+    import gdn_cases as gc
+
+    x, z, w, eps = gc.rmsnorm_inputs()
+    per = _bytes(x, z, w)
+    sets = rotation(lambda: (x, z, w), per, dev)
+    ms = time_calls(lambda i: ops.gated_rmsnorm(sets[i][0], sets[i][1], sets[i][2], eps),
+                    len(sets), steps, warmup)
+    algo = per + _bytes(x)
+    return dict(ms=ms, gbs=algo / ms / 1e6, frac=algo / ms / 1e6 / HBM_PEAK_GBS, bytes=algo)
+
+
+# Algorithmic FLOPs per chunk-head of each prefill kernel (C = 64, dk = dv = 128,
+# 2 FLOP per MAC): prep forms K K^T, Q K^T, T (v beta), T (k beta e^c) and the
+# inversion (C^3/3 MACs); scan forms W S, (Q e^c) S, K~^T V_new and M V_new.
+_CC = 2 * 64 * 64 * 128          # one C x C x 128 product
+_CD = 2 * 64 * 128 * 128         # one 64 x 128 x 128 product
+_INV = 2 * 64 ** 3 // 3
+KERNEL_FLOPS_PER_CHUNK_HEAD = {"gdn_prep_kernel": 4 * _CC + _INV,
+                               "gdn_scan_kernel": 3 * _CD + _CC}
+
+
+class _Hip:
+    """hipEvent_t helpers over libamdhip64 (the events the library records)."""
+
+    def __init__(self):
+        import ctypes as ct
+
+        self.ct = ct
+        self.rt = ct.CDLL("libamdhip64.so")
+        self.rt.hipEventCreate.argtypes = [ct.POINTER(ct.c_void_p)]
+        self.rt.hipEventElapsedTime.argtypes = [ct.POINTER(ct.c_float), ct.c_void_p, ct.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ct.c_void_p]
+
+    def events(self, n):
+        evs = (self.ct.c_void_p * n)()
+        for i in range(n):
+            ev = self.ct.c_void_p()
+            assert self.rt.hipEventCreate(self.ct.byref(ev)) == 0
+            evs[i] = ev
+        return evs
+
+    def elapsed_ms(self, a, b):
+        ms = self.ct.c_float()
+        assert self.rt.hipEventElapsedTime(self.ct.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.rt.hipEventDestroy(e)
+
+
+def kernel_times(dev, steps, warmup):
+    """Average duration of each prefill kernel at T=1141 HV=32, from HIP events the
+    library records on the launch stream between its kernels
+    (deltanet_chunk_prefill_timed), over `steps` cold calls."""
+    import torch
+    import gdn_cases as gc
+    from gdn_hip import capi
+
+    lib = capi.lib()
+    hip = _Hip()
+    nk = lib.deltanet_prefill_kernel_count()
+    names = [lib.deltanet_prefill_kernel_name(i).decode() for i in range(nk)]
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    B, T, HK, D = q.shape
+    HV = v.shape[2]
+    sets = rotation(lambda: (q, k, v, g, beta, s0), _bytes(q, k, v, g, beta, s0), dev)
+    wsb = lib.deltanet_prefill_workspace_size(B, T, HV, D, D, 64)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    o = torch.empty_like(sets[0][2])
+    sf = torch.empty_like(sets[0][5])
+    stream = torch.cuda.current_stream().cuda_stream
+    n = warmup + steps
+    evs = [hip.events(nk + 1) for _ in range(n)]
+    for i in range(n):
+        qq, kk, vv, gg, bb, ss = sets[i % len(sets)]
+        err = lib.deltanet_chunk_prefill_timed(
+            qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), gg.data_ptr(), bb.data_ptr(),
+            o.data_ptr(), ss.data_ptr(), sf.data_ptr(), B, T, HV, HK, D, D, 64,
+            ws.data_ptr(), wsb, stream, evs[i], nk + 1)
+        assert err == 0, f"deltanet_chunk_prefill_timed returned {err}"
+    torch.cuda.synchronize()
+    tot = [0.0] * nk
+    for i in range(warmup, n):
+        for j in range(nk):
+            tot[j] += hip.elapsed_ms(evs[i][j], evs[i][j + 1])
+    for e in evs:
+        hip.destroy(e)
+    nch = B * ((T + 63) // 64) * HV
+    return {nm: dict(ms=t / steps, flops=KERNEL_FLOPS_PER_CHUNK_HEAD[nm] * nch)
+            for nm, t in zip(names, tot)}
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch of `kernel` (T=1141, HV=32 prefill) from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of
+    known size), or None when no summary exists for it."""
+    import re
+
+    p = ROOT / "profiles" / f"{kernel}_T1141_HV32_traffic.md"
+    if not p.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text(), flags=re.M)
+    return float(m.group(1)) if m else None
+
+
+def profile_pass(ops, dev):
+    """Work for a counter run: cold T=1141 HV=32 prefill calls, then a copy of known
+    size (torch.neg over 256 MiB fp32: 256 MiB read + 256 MiB written)."""
+    import torch
+    import gdn_cases as gc
+
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    sets = rotation(lambda: (q, k, v, g, beta, s0), _bytes(q, k, v, g, beta, s0), dev)
+    for i in range(4):
+        ops.chunk_prefill(*sets[(7 * i) % len(sets)])
+    torch.cuda.synchronize()
+    del sets
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("profile pass done: 4 prefill calls (T=1141, HV=32), 2 x torch.neg over 256 MiB", flush=True)
+
+
+def cpu_baseline(budget_s=12.0):
+    """The CPU oracle (fp32 torch restatement of the reference's torch path)
+    on the same T=1141 HV=32 inputs, host cores; median of >= 3 timed calls."""
+    import torch
+    import gdn_cases as gc
+    from oracle import gdn_oracle as orc
+
+    # the host share of one GPU is at most 16 cores, whatever os.cpu_count() says
+    torch.set_num_threads(max(1, min(16, int(os.environ.get("OMP_NUM_THREADS", "16")),
+                                     os.cpu_count() or 1)))
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    run = lambda: orc.chunk_gated_delta_rule(q, k, v, g, beta, s0, dtype=torch.float32)  # noqa: E731
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    ms = times[len(times) // 2] * 1e3
+    flops = gc.flops_prefill(q.shape[1], v.shape[2])
+    return dict(value=round(flops / ms / 1e9, 6), unit="TFLOP/s", ms_per_call=round(ms, 3),
+                cores=torch.get_num_threads(), kind="port",
+                sample=f"full prefill call (T=1141, HV=32), fp32 torch CPU oracle, median of {len(times)}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="no timing: 4 cold T=1141 HV=32 prefill calls, then 2 elementwise copies of "
+                         "256 MiB (the calibration for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the gated-delta hot path is built and measured on a "
+              "single MI355X (heads shard with no exchange across GPUs); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gdn_hip
+
+    ops = gdn_hip.load()
+    dev = torch.device("cuda:0")
+    if args.profile_pass:
+        profile_pass(ops, dev)
+        return
+    pre = bench_prefill(ops, dev, args.steps, args.warmup)
+    ms = pre["cold_ms"]
+    tflops = pre["flops"] / ms / 1e9
+    gbs = pre["algo_bytes"] / ms / 1e6
+    line = {
+        "metric": "gated-delta prefill µs + TFLOP/s (T=1141,H=32,d=128); % MFMA/HBM roofline",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_call": round(ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn; q/k l2-normalised; beta=sigmoid, g=logsigmoid(x+2))",
+        "config": {"workload": "chunked gated-delta prefill, one layer", "B": 1, "T": pre["T"],
+                   "HV": pre["HV"], "HK": 16, "dk": 128, "dv": 128, "chunk": 64,
+                   "inputs": f"rotated over {pre['n_sets']} resident copies (cold)"},
+        "warm": {"us_per_call": round(pre["warm_ms"] * 1e3, 2),
+                 "tflops": round(pre["flops"] / pre["warm_ms"] / 1e9, 3)},
+        "roofline_whole_call": {
+            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "algo_flops": pre["flops"], "algo_bytes": pre["algo_bytes"]},
+    }
+    kt = kernel_times(dev, args.steps, args.warmup)
+    dom = max(kt, key=lambda nm: kt[nm]["ms"])
+    ach = kt[dom]["flops"] / kt[dom]["ms"] / 1e9
+    line["roofline"] = {
+        "kernel": dom, "bound": "mfma", "achieved": round(ach, 3), "peak": MFMA_PEAK_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(ach / MFMA_PEAK_TFLOPS, 5),
+        "traffic": traffic_from_profiles(dom),
+        "us_per_launch": round(kt[dom]["ms"] * 1e3, 2),
+        "kernels_us": {nm: round(d["ms"] * 1e3, 2) for nm, d in kt.items()},
+    }
+    if not args.no_secondary:
+        nrm = bench_norm(ops, dev, args.steps, args.warmup)
+        dec = bench_decode(ops, dev, max(20, args.steps // 4), args.warmup)
+        var = bench_varlen(ops, dev, max(10, args.steps // 10), 5)
+        line["secondary"] = {
+            "gated_rmsnorm_1141x32x128": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
+                                 "hbm_frac": round(nrm["frac"], 4)},
+            "decode_B64_HV32": {"us": round(dec["ms"] * 1e3, 2), "GB/s": round(dec["gbs"], 1),
+                          "hbm_frac": round(dec["frac"], 4)},
+            "varlen_prefill_8seq_19861tok": {"us": round(var["ms"] * 1e3, 2),
+                                  "TFLOP/s": round(var["tflops"], 3),
+                                  "tokens": var["tokens"]},
+        }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -52,6 +52,22 @@ hipError_t deltanet_chunk_prefill(const void* q, const void* k, const void* v, c
                                   int DV, int chunk_size, void* workspace, size_t workspace_bytes,
                                   hipStream_t stream, int dump_debug);
 
+/* Per-kernel timing of deltanet_chunk_prefill (no counterpart in the
+ * reference; for benchmarks that attribute time to each kernel).
+ * deltanet_prefill_kernel_count() kernels are launched; events[i] is recorded
+ * on `stream` before kernel i and events[count] after the last, so
+ * hipEventElapsedTime(events[i], events[i + 1]) is kernel i's duration.
+ * n_events must equal count + 1; the other arguments are as in
+ * deltanet_chunk_prefill (dump_debug = 0). */
+int deltanet_prefill_kernel_count(void);
+const char* deltanet_prefill_kernel_name(int i);
+hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k, const void* v,
+                                        const float* g, const float* beta, void* o,
+                                        const float* initial_state, float* final_state, int B,
+                                        int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                        void* workspace, size_t workspace_bytes,
+                                        hipStream_t stream, hipEvent_t* events, int n_events);
+
 /* Names of the reference's bf16-wmma o-pass twin (kernels/chunk_delta_cuda_tco.h:39,47);
  * same implementation and workspace as the two entries above. */
 size_t deltanet_tcop_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int chunk_size);

@@ -706,7 +706,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
                           const float* beta, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
-                          hipStream_t stream, int dump_debug) {
+                          hipStream_t stream, int dump_debug, hipEvent_t* ev = nullptr) {
     const WsLayout L(nch_bound * (size_t)HV);
     if (workspace_bytes < L.total) return hipErrorInvalidValue;
     char* base = static_cast<char*>(workspace);
@@ -722,6 +722,8 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     ws.dbgC = dump_debug ? reinterpret_cast<float*>(base + L.dbgC) : nullptr;
     const float scale = 1.0f / sqrtf((float)kDK);
 
+    // ev (optional): kPrefillKernels + 1 events recorded around the launches
+    if (ev) hipEventRecord(ev[0], stream);
     if (nch_bound > 0 && total_tokens > 0) {
         hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nch_bound, HV), dim3(kPrepThreads), 0,
                            stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
@@ -729,12 +731,18 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
+    if (ev) hipEventRecord(ev[1], stream);
     const int pairs = N * HV;
     const int groups = (pairs + 7) / 8;
     hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 64)), dim3(kScanThreads), 0, stream,
                        ws, static_cast<uint16_t*>(o), s0, sf, cu, N, T, HV);
-    return hipGetLastError();
+    hipError_t err = hipGetLastError();
+    if (ev) hipEventRecord(ev[2], stream);
+    return err;
 }
+
+constexpr int kPrefillKernels = 2;
+const char* const kPrefillKernelNames[kPrefillKernels] = {"gdn_prep_kernel", "gdn_scan_kernel"};
 
 bool dims_ok(int HV, int HQK, int DK, int DV, int chunk_size) {
     return DK == kDK && DV == kDV && chunk_size == kChunk && HQK > 0 && HV > 0 && HV % HQK == 0;
@@ -765,6 +773,31 @@ extern "C" hipError_t deltanet_chunk_prefill(const void* q, const void* k, const
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
     return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
                           HV, HQK, nc, workspace, workspace_bytes, stream, dump_debug);
+}
+
+extern "C" int deltanet_prefill_kernel_count(void) { return kPrefillKernels; }
+
+extern "C" const char* deltanet_prefill_kernel_name(int i) {
+    return (i >= 0 && i < kPrefillKernels) ? kPrefillKernelNames[i] : nullptr;
+}
+
+extern "C" hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k, const void* v,
+                                                   const float* g, const float* beta, void* o,
+                                                   const float* initial_state,
+                                                   float* final_state, int B, int T, int HV,
+                                                   int HQK, int DK, int DV, int chunk_size,
+                                                   void* workspace, size_t workspace_bytes,
+                                                   hipStream_t stream, hipEvent_t* events,
+                                                   int n_events) {
+    if (!events || n_events != kPrefillKernels + 1) return hipErrorInvalidValue;
+    for (int i = 0; i < n_events; ++i)
+        if (!events[i]) return hipErrorInvalidValue;
+    if (!dims_ok(HV, HQK, DK, DV, chunk_size) || B <= 0 || T < 0) return hipErrorInvalidValue;
+    if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
+                          HV, HQK, nc, workspace, workspace_bytes, stream, 0, events);
 }
 
 extern "C" size_t deltanet_prefill_varlen_workspace_size(int total_tokens, int num_seqs, int HV,

@@ -35,6 +35,10 @@ _PROTOS = {
                                       [c_int] * 7 + [vp, c_size_t, hipStream_t, c_int]),
     "deltanet_recurrent_step": (hipError_t, [vp, vp, vp, fp, fp, vp, fp] + [c_int] * 6 +
                                 [hipStream_t]),
+    "deltanet_prefill_kernel_count": (c_int, []),
+    "deltanet_prefill_kernel_name": (ct.c_char_p, [c_int]),
+    "deltanet_chunk_prefill_timed": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
+                                     [vp, c_size_t, hipStream_t, vp, c_int]),
     "gdn_gated_rmsnorm_forward": (hipError_t, [vp, vp, vp, vp, c_int64, c_int, c_float, c_int,
                                                c_int, hipStream_t]),
 }
@@ -44,7 +48,8 @@ def declared_symbols() -> list[str]:
     """Function names declared in include/gdn_hip.h."""
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^\s*(?:size_t|hipError_t)\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:size_t|hipError_t|int|const char\s*\*)\s*(\w+)\s*\(", text,
+                      flags=re.M)
 
 
 _lib = None

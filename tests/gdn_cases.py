@@ -1,14 +1,14 @@
 """Seeded inputs and parity metrics shared by the tests, smoke() and bench.py.
 
-Input generators follow the five workload definitions of this path (all CPU
+Input generators for the five workloads of this path (all CPU
 ``torch.Generator`` draws, in the order q, k, v, beta, g, state, so the same
 tensors can be moved to the GPU and handed to the oracle):
 
-  c1  CPU plumbing         B1 T256 H4 d64 fp32, chunk 64, seed 0
-  c2  gated RMSNorm        rows 1141x32, d128 bf16, seed 1
-  c3  decode step          B64 T1 HV32 HK16 d128, seed 3
-  c4  chunked prefill      B1 T1141 HV32 HK16 d128, seed 4
-  c5  varlen prefill       8 sequences, lengths from seed 7, seed 5 for tensors
+  plumbing_inputs  CPU plumbing      B1 T256 H4 d64 fp32, chunk 64, seed 0
+  rmsnorm_inputs   gated RMSNorm     rows 1141x32, d128 bf16, seed 1
+  decode_inputs    decode step       B64 T1 HV32 HK16 d128, seed 3
+  prefill_inputs   chunked prefill   B1 T1141 HV32 HK16 d128, seed 4
+  varlen_inputs    varlen prefill    8 sequences, lengths from seed 7, seed 5 for tensors
 
 ``make_reference_inputs`` restates the reference harness's random grid
 (kernels/harness/parity_test.py:102-121) on a CPU generator.
@@ -28,7 +28,7 @@ ABS_TOL = 2e-2          # max |err| bar on o and final state (fp32-accumulated b
 REF_COS_MIN = 0.999     # reference harness random-case bar (parity_test.py:188-189)
 REF_REL_MAX = 1e-2
 
-C4_LENGTHS_SEED = 7
+VARLEN_LENGTHS_SEED = 7
 
 
 def l2norm(x, eps=1e-6):
@@ -54,7 +54,7 @@ def make_gdn_inputs(seed, B, T, HK, HV, D=128, g_shift=0.0, g_offset=0.0, s0_sca
     return q, k, v, g, beta, s0
 
 
-def c1_inputs():
+def plumbing_inputs():
     gen = _gen(0)
     B, T, H, D = 1, 256, 4, 64
     q = l2norm(torch.randn(B, T, H, D, generator=gen))
@@ -66,7 +66,7 @@ def c1_inputs():
     return q, k, v, g, beta, s0
 
 
-def c2_inputs(rows_t=1141, heads=32, dv=128):
+def rmsnorm_inputs(rows_t=1141, heads=32, dv=128):
     gen = _gen(1)
     x = torch.randn(rows_t, heads, dv, generator=gen).to(torch.bfloat16)
     z = torch.randn(rows_t, heads, dv, generator=gen).to(torch.bfloat16)
@@ -74,20 +74,20 @@ def c2_inputs(rows_t=1141, heads=32, dv=128):
     return x, z, w, 1e-6
 
 
-def c3_inputs():
+def decode_inputs():
     return make_gdn_inputs(3, B=64, T=1, HK=16, HV=32, g_offset=-1.0)
 
 
-def c4_inputs():
+def prefill_inputs():
     return make_gdn_inputs(4, B=1, T=1141, HK=16, HV=32, g_shift=2.0)
 
 
-def c5_lengths():
-    return torch.randint(512, 4097, (8,), generator=_gen(C4_LENGTHS_SEED))
+def varlen_lengths():
+    return torch.randint(512, 4097, (8,), generator=_gen(VARLEN_LENGTHS_SEED))
 
 
-def c5_inputs(lengths=None):
-    lengths = c5_lengths() if lengths is None else torch.as_tensor(lengths)
+def varlen_inputs(lengths=None):
+    lengths = varlen_lengths() if lengths is None else torch.as_tensor(lengths)
     total = int(lengths.sum())
     q, k, v, g, beta, s0 = make_gdn_inputs(5, B=1, T=total, HK=16, HV=32, g_shift=2.0,
                                            n_states=len(lengths))

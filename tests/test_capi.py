@@ -1,0 +1,126 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every function
+include/gdn_hip.h declares, sizes workspaces, and rejects unsupported
+configurations on the host (hipErrorInvalidValue, the reference's
+cudaErrorInvalidValue contract, kernels/chunk_delta_cuda.cu:706-708,727)
+before any launch.  No call here reaches a kernel."""
+import ctypes as ct
+
+import pytest
+
+import gdn_hip
+from gdn_hip import capi
+
+INVALID = capi.HIP_ERROR_INVALID_VALUE
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not gdn_hip.LIB_PATH.exists():
+        pytest.fail(f"{gdn_hip.LIB_PATH} is not built")
+    return capi.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = capi.declared_symbols()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/gdn_hip.h but not exported"
+        assert n in capi._PROTOS, f"{n} has no ctypes prototype"
+
+
+def test_workspace_size(lib):
+    ws = lib.deltanet_prefill_workspace_size
+    assert ws(1, 1141, 32, 128, 128, 64) > 0
+    assert ws(1, 1141, 32, 64, 128, 64) == 0          # DK != 128
+    assert ws(1, 1141, 32, 128, 64, 64) == 0          # DV != 128
+    assert ws(1, 1141, 32, 128, 128, 32) == 0         # chunk != 64
+    assert ws(0, 10, 32, 128, 128, 64) == 0
+    # grows with chunks and heads; tcop twin is the same size
+    assert ws(1, 1152, 32, 128, 128, 64) == ws(1, 1141, 32, 128, 128, 64)
+    assert ws(1, 1153, 32, 128, 128, 64) > ws(1, 1152, 32, 128, 128, 64)
+    assert ws(2, 1141, 32, 128, 128, 64) > ws(1, 1141, 32, 128, 128, 64)
+    assert lib.deltanet_tcop_prefill_workspace_size(1, 1141, 32, 128, 128, 64) == \
+        ws(1, 1141, 32, 128, 128, 64)
+    # varlen bound covers every split of the tokens into num_seqs sequences
+    vws = lib.deltanet_prefill_varlen_workspace_size
+    lens = [1427, 3804, 2613, 3898, 660, 2279, 4069, 1111]
+    chunks = sum((n + 63) // 64 for n in lens)
+    assert vws(sum(lens), 8, 32, 128, 128, 64) >= ws(1, 64 * chunks, 32, 128, 128, 64)
+    assert vws(8 * 65, 8, 32, 128, 128, 64) >= ws(1, 64 * 16, 32, 128, 128, 64)
+    assert vws(100, 0, 32, 128, 128, 64) == 0
+
+
+def _prefill_args(**over):
+    a = dict(q=1, k=1, v=1, g=1, beta=1, o=1, s0=None, sf=1, B=1, T=64, HV=4, HQK=2, DK=128,
+             DV=128, chunk=64, ws=1, ws_bytes=1 << 40, stream=None, dbg=0)
+    a.update(over)
+    return a
+
+
+def _call_prefill(lib, a):
+    return lib.deltanet_chunk_prefill(a["q"], a["k"], a["v"], a["g"], a["beta"], a["o"], a["s0"],
+                                      a["sf"], a["B"], a["T"], a["HV"], a["HQK"], a["DK"],
+                                      a["DV"], a["chunk"], a["ws"], a["ws_bytes"], a["stream"],
+                                      a["dbg"])
+
+
+@pytest.mark.parametrize("bad", [dict(DK=64), dict(DV=256), dict(chunk=32), dict(HQK=3),
+                                 dict(HV=0), dict(B=0), dict(T=-1), dict(ws=None),
+                                 dict(sf=None), dict(q=None), dict(ws_bytes=16)])
+def test_prefill_rejects_on_host(lib, bad):
+    assert _call_prefill(lib, _prefill_args(**bad)) == INVALID
+
+
+def test_timed_prefill_rejects_bad_events(lib):
+    n = lib.deltanet_prefill_kernel_count()
+    assert n >= 1
+    assert all(lib.deltanet_prefill_kernel_name(i) for i in range(n))
+    assert lib.deltanet_prefill_kernel_name(n) is None
+    ev = (ct.c_void_p * (n + 1))()
+    a = _prefill_args()
+    args = [a[x] for x in ("q", "k", "v", "g", "beta", "o", "s0", "sf", "B", "T", "HV", "HQK",
+                           "DK", "DV", "chunk", "ws", "ws_bytes", "stream")]
+    assert lib.deltanet_chunk_prefill_timed(*args, None, n + 1) == INVALID
+    assert lib.deltanet_chunk_prefill_timed(*args, ev, n) == INVALID
+    assert lib.deltanet_chunk_prefill_timed(*args, ev, n + 1) == INVALID   # null events
+
+
+def test_varlen_rejects_on_host(lib):
+    f = lib.deltanet_chunk_prefill_varlen
+    ok = [1, 1, 1, 1, 1, 1, None, 1, 1, 2, 128, 4, 2, 128, 128, 64, 1, 1 << 40, None, 0]
+    bad_cu = list(ok)
+    bad_cu[8] = None
+    assert f(*bad_cu) == INVALID
+    bad_n = list(ok)
+    bad_n[9] = 0
+    assert f(*bad_n) == INVALID
+    bad_dk = list(ok)
+    bad_dk[13] = 64
+    assert f(*bad_dk) == INVALID
+
+
+def test_decode_and_norm_reject_on_host(lib):
+    dec = lib.deltanet_recurrent_step
+    assert dec(1, 1, 1, 1, 1, 1, 1, 2, 1, 4, 3, 128, 128, None) == INVALID   # HV % HQK
+    assert dec(1, 1, 1, 1, 1, 1, 1, 2, 1, 4, 2, 64, 128, None) == INVALID    # DK
+    assert dec(1, 1, 1, 1, 1, 1, None, 2, 1, 4, 2, 128, 128, None) == INVALID
+    nrm = lib.gdn_gated_rmsnorm_forward
+    assert nrm(1, 1, 1, 1, 10, 96, 1e-6, capi.DTYPE_BF16, capi.DTYPE_BF16, None) == INVALID
+    assert nrm(1, 1, 1, 1, 10, 128, 1e-6, capi.DTYPE_FP32, capi.DTYPE_FP32, None) == INVALID
+    assert nrm(1, 1, 1, 1, 10, 128, 1e-6, capi.DTYPE_BF16, capi.DTYPE_FP16, None) == INVALID
+    assert nrm(None, 1, 1, 1, 10, 128, 1e-6, capi.DTYPE_BF16, capi.DTYPE_BF16, None) == INVALID
+
+
+def test_torch_extension_loads_and_checks_device():
+    import torch
+
+    ops = gdn_hip.load()
+    for name in ("chunk_prefill", "chunk_prefill_debug", "recurrent_step", "gated_rmsnorm"):
+        assert hasattr(ops, name)
+    q = torch.zeros(1, 64, 2, 128, dtype=torch.bfloat16)
+    v = torch.zeros(1, 64, 4, 128, dtype=torch.bfloat16)
+    g = torch.zeros(1, 64, 4)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        ops.chunk_prefill(q, q, v, g, g, None)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        ops.gated_rmsnorm(v, v, torch.ones(128, dtype=torch.bfloat16), 1e-6)

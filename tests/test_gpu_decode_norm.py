@@ -23,9 +23,9 @@ def _decode_check(ops, dev, q, k, v, g, beta, s0, tag):
     return o, state
 
 
-def test_c3_decode(ops, dev):
+def test_decode_B64_HV32(ops, dev):
     """B64 T1 HV32 HK16 d128, fp32 state updated in place."""
-    _decode_check(ops, dev, *gc.c3_inputs(), tag="c3")
+    _decode_check(ops, dev, *gc.decode_inputs(), tag="decode B64 HV32")
 
 
 @pytest.mark.parametrize("T", [2, 5])
@@ -70,9 +70,9 @@ def _norm_check(ops, dev, x, z, w, eps, tag):
     return y
 
 
-def test_c2_gated_rmsnorm(ops, dev):
+def test_gated_rmsnorm_1141x32(ops, dev):
     """rows 1141x32, d128, bf16 o/z/w, eps 1e-6 (HF Qwen3_5RMSNormGated rounding)."""
-    _norm_check(ops, dev, *gc.c2_inputs(), tag="c2")
+    _norm_check(ops, dev, *gc.rmsnorm_inputs(), tag="rmsnorm 1141x32x128")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

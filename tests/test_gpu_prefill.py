@@ -36,15 +36,29 @@ def _run_and_check(ops, dev, q, k, v, g, beta, s0, tag, ref_bar=True, cu=None):
     return o, sf
 
 
-def test_c4_planner_shape(ops, dev):
+def test_prefill_T1141_HV32(ops, dev):
     """B1 T1141 HV32 HK16 d128: ragged 53-row tail chunk, GQA 2:1."""
-    _run_and_check(ops, dev, *gc.c4_inputs(), tag="c4")
+    _run_and_check(ops, dev, *gc.prefill_inputs(), tag="prefill T1141 HV32")
 
 
-def test_c5_varlen(ops, dev):
+def test_golden_g128(ops, dev):
+    """Committed fixture (tests/golden/g128.npz): fp64 recurrence outputs."""
+    from test_golden import g128_inputs
+
+    q, k, v, g, beta, s0, o_ref, s_ref = g128_inputs()
+    print(f"[prefill] golden g128 q={tuple(q.shape)} v={tuple(v.shape)}", flush=True)
+    o, sf = ops.chunk_prefill(*[t.to(dev) for t in (q, k, v, g, beta, s0)])
+    torch.cuda.synchronize()
+    mo, ms = gc.parity(o, o_ref), gc.parity(sf, s_ref)
+    print(f"    o: {gc.fmt(mo)}\n    S: {gc.fmt(ms)}", flush=True)
+    gc.assert_abs(mo, what="g128 o")
+    gc.assert_abs(ms, what="g128 state")
+
+
+def test_varlen_8_sequences(ops, dev):
     """8 sequences of seed-7 lengths (sum 19861), independent initial states."""
-    q, k, v, g, beta, s0, cu = gc.c5_inputs()
-    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="c5", cu=cu)
+    q, k, v, g, beta, s0, cu = gc.varlen_inputs()
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="varlen 8 seqs", cu=cu)
 
 
 @pytest.mark.parametrize("T", [1, 2, 17, 63, 64, 65, 127, 128, 200])
@@ -82,7 +96,7 @@ def test_reference_grid_init_state(ops, dev):
 def test_varlen_edges(ops, dev):
     """Empty, single-token and chunk-boundary lengths in one packed batch."""
     lens = torch.tensor([0, 1, 63, 64, 65, 0, 130, 5])
-    q, k, v, g, beta, s0, cu = gc.c5_inputs(lens)
+    q, k, v, g, beta, s0, cu = gc.varlen_inputs(lens)
     o, sf = _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="varlen-edges", cu=cu)
     # empty sequences pass their initial state through unchanged
     assert torch.equal(sf[0].cpu(), s0[0].float())
@@ -90,9 +104,9 @@ def test_varlen_edges(ops, dev):
 
 
 def test_varlen_equals_per_sequence_calls(ops, dev):
-    """Size-independent property at the c5 size: the packed call is bitwise the
+    """Size-independent property at the 8-sequence varlen size: the packed call is bitwise the
     per-sequence fixed-length calls (same chunking, same kernels)."""
-    q, k, v, g, beta, s0, cu = gc.c5_inputs()
+    q, k, v, g, beta, s0, cu = gc.varlen_inputs()
     d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
     o, sf = ops.chunk_prefill(*d, cu_seqlens=cu.to(dev))
     for i in range(len(cu) - 1):
@@ -105,7 +119,7 @@ def test_varlen_equals_per_sequence_calls(ops, dev):
 
 def test_gqa_equals_expanded_heads(ops, dev):
     """HK=16 -> HV=32 sharing is bitwise the explicit repeat_interleave."""
-    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.c4_inputs()]
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.prefill_inputs()]
     o1, s1 = ops.chunk_prefill(q, k, v, g, beta, s0)
     o2, s2 = ops.chunk_prefill(q.repeat_interleave(2, 2), k.repeat_interleave(2, 2), v, g, beta, s0)
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
@@ -114,7 +128,7 @@ def test_gqa_equals_expanded_heads(ops, dev):
 def test_resume_split(ops, dev):
     """Running [0, 640) then [640, T) from the carried state matches one call
     (chunk-aligned split, so the chunking is identical: bitwise)."""
-    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.c4_inputs()]
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.prefill_inputs()]
     o, sf = ops.chunk_prefill(q, k, v, g, beta, s0)
     t = 640
     oa, sa = ops.chunk_prefill(q[:, :t], k[:, :t], v[:, :t], g[:, :t], beta[:, :t], s0)
