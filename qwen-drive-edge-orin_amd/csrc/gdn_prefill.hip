@@ -15,17 +15,23 @@
 // kernels/chunk_delta_cuda.cu:91-303 and :312-424 compute the same terms.)
 //
 // Two kernels:
-//   prep  grid (chunks, HV):  all chunk-local work.  Writes W, decayed K^T,
-//         scaled Q and M as fp16 MFMA A-operand fragments and U as fp32
-//         accumulator fragments, so the scan issues one 16-byte load per lane
-//         per fragment and never reshuffles.
-//   scan  grid (8 slices x HV x sequences): the state S of one head is split
-//         into 8 slices of 16 columns (columns of S evolve independently).
-//         Wave 0 runs the serial chain V_n = U - W S, S <- d S + K~^T V_n
-//         with the slice in registers for the whole sequence; wave 1 forms
-//         O = Q~ S + M V_n from S and V_n handed over through a 2-deep LDS
-//         ring.  Work-group ids are laid out so the 8 slices of a head land
-//         on one XCD and share its L2.
+//   prep  one work-group per (chunk, v-head), three per CU: all chunk-local
+//         work.  K K^T and K Q^T run on bf16 MFMA straight from the bf16
+//         inputs; the inverse T is formed in fp32 in one LDS array (16x16
+//         diagonal blocks by forward substitution, off-diagonal blocks on
+//         fp32 MFMA, stored transposed in the free upper triangle).  Writes
+//         W, decayed K^T and M as fp16 MFMA A-operand fragments and U as
+//         fp16 accumulator fragments, so the scan moves each operand with
+//         one 16-byte transfer per lane and never reshuffles.
+//   scan  one work-group per (state slice, v-head, sequence): the state of a
+//         head is split into 8 slices of 16 value columns, which evolve
+//         independently.  Wave 0 runs the serial chain with its 128x16 fp32
+//         slice in registers; it streams W, K~^T and U for chunk c+2 into a
+//         3-stage LDS ring with LDS-direct loads while computing chunk c.
+//         Six output waves take every sixth chunk and form
+//         O = (s e^c Q) S + M V_n from S and V_n handed over through LDS
+//         slots guarded by counters; each has six chain steps to cover its
+//         own load latency, so the chain never waits for outputs.
 #include "gdn_common.h"
 #include "gdn_hip.h"
 
@@ -35,22 +41,25 @@ namespace gdn {
 namespace {
 
 constexpr int kPrepThreads = 256;
-constexpr int kScanThreads = 128;
+// scan work-group: wave 0 runs the chain, waves 4-6 load its operands,
+// waves 1-3 and 7 form outputs
+constexpr int kScanThreads = 512;
+constexpr int kOutWaves = 4;
 
 // Per chunk-head record sizes (elements)
-constexpr int kWfElems = kChunk * kDK;      // fp16, 16 fragments of 64 lanes x 8
-constexpr int kKfElems = kDK * kChunk;      // fp16, 16 fragments
-constexpr int kQfElems = kChunk * kDK;      // fp16, 16 fragments
-constexpr int kMfElems = kChunk * kChunk;   // fp16, 8 fragments
-constexpr int kUfElems = kChunk * kDV;      // fp32, 8 slices x 4 tiles x 64 lanes x 4
+constexpr int kWfElems = kChunk * kDK;     // fp16: W, 16 A-fragments (4 row tiles x 4 k-blocks)
+constexpr int kKfElems = kDK * kChunk;     // fp16: decayed K^T, 16 A-fragments (8 dk tiles x 2 k-blocks)
+constexpr int kUfElems = kChunk * kDV;     // fp16: U in accumulator order, 8 slices x 2 tile pairs
+constexpr int kMfElems = kChunk * kChunk;  // fp16: M, 8 A-fragments (4 row tiles x 2 k-blocks)
+constexpr int kGateFloats = 128;           // fp32: s e^c [64] | e^{c_63} | unused
+constexpr int kGateDecay = 64;
 
 struct Workspace {
     _Float16* Wf;
     _Float16* Kf;
-    _Float16* Qf;
+    _Float16* Uf;
     _Float16* Mf;
-    float* Uf;
-    float* decay;
+    float* gates;
     float* dbgT;   // optional: T = (I-A)^-1, [chunk-head][64][64]
     float* dbgA;   // optional: A, same layout
     float* dbgC;   // optional: in-chunk cumsum of g, [chunk-head][64]
@@ -58,17 +67,17 @@ struct Workspace {
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Byte layout of the workspace for `nch` chunk-heads.
+// Byte layout of the workspace for `nch` chunk-heads.  The three debug
+// regions stay last: the torch binding finds them from the end.
 struct WsLayout {
-    size_t wf, kf, qf, mf, uf, decay, dbgT, dbgA, dbgC, total;
+    size_t wf, kf, uf, mf, gates, dbgT, dbgA, dbgC, total;
     __host__ explicit WsLayout(size_t nch) {
         size_t off = 0;
         wf = off;    off += align256(nch * kWfElems * 2);
         kf = off;    off += align256(nch * kKfElems * 2);
-        qf = off;    off += align256(nch * kQfElems * 2);
+        uf = off;    off += align256(nch * kUfElems * 2);
         mf = off;    off += align256(nch * kMfElems * 2);
-        uf = off;    off += align256(nch * kUfElems * 4);
-        decay = off; off += align256(nch * 4);
+        gates = off; off += align256(nch * kGateFloats * 4);
         dbgT = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgA = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgC = off;  off += align256(nch * kChunk * 4);
@@ -91,7 +100,6 @@ __device__ int chunks_before(const int32_t* cu, int T, int upto, int* red) {
     if (!cu) return upto * ((T + kChunk - 1) / kChunk);
     int acc = 0;
     for (int s = threadIdx.x; s < upto; s += NT) acc += (cu[s + 1] - cu[s] + kChunk - 1) / kChunk;
-    // wave reduce then cross-wave through LDS
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
@@ -103,7 +111,8 @@ __device__ int chunks_before(const int32_t* cu, int T, int upto, int* red) {
 }
 
 // Block-cooperative: map global chunk id -> (sequence, first token, rows).
-// Returns false (uniformly) when cid is past the last chunk.
+// Returns false (uniformly) when cid is past the last chunk.  `red` holds NT
+// ints of scratch.
 template <int NT>
 __device__ bool locate_chunk(const int32_t* cu, int N, int T, int cid, int* red,
                              int& seq, int& tok0, int& rows) {
@@ -166,91 +175,127 @@ __device__ inline half8 bf16x8_to_half8(uint4 raw) {
     return h;
 }
 
-__device__ inline half4 bf16x4_to_half4(uint2 raw) {
-    half4 h;
-    h[0] = (_Float16)bf16_bits_to_f32(raw.x & 0xffffu);
-    h[1] = (_Float16)bf16_bits_to_f32(raw.x >> 16);
-    h[2] = (_Float16)bf16_bits_to_f32(raw.y & 0xffffu);
-    h[3] = (_Float16)bf16_bits_to_f32(raw.y >> 16);
-    return h;
+// Two 4-element bf16 pieces (k-map registers 0..3 and 4..7) as one operand
+__device__ inline bf16x8 bf16_frag(uint2 lo, uint2 hi) {
+    const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
+    return __builtin_bit_cast(bf16x8, w);
 }
+
+__device__ inline half8 bf16_frag_to_half8(uint2 lo, uint2 hi) {
+    const uint4 w = {lo.x, lo.y, hi.x, hi.y};
+    return bf16x8_to_half8(w);
+}
+
+__device__ __forceinline__ f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
 // prep kernel: one work-group (4 waves) per (chunk, v-head)
 // ---------------------------------------------------------------------------
-constexpr int kKrStride = kDK + 8;      // fp16 row-major K  [64][136]
-constexpr int kKtStride = kChunk + 8;   // fp16 K^T / V^T    [128][72]
-constexpr int kMatStride = kChunk + 4;  // fp32 A / T        [64][68]
+constexpr int kKS = kDK + 8;      // bf16 K row pitch: 136 halves (272 B, 16-byte aligned)
+constexpr int kTS = kChunk + 4;   // fp16 V^T row pitch: 68 halves
+constexpr int kMS = kChunk + 4;   // fp32 A / T row pitch: 68 floats
 
 struct PrepSmem {
-    _Float16 Kr[kChunk * kKrStride];
-    _Float16 Kt[kDK * kKtStride];
-    union {
-        float A[kChunk * kMatStride];       // A, live until the inverse is done
-        _Float16 Vt[kDV * kKtStride];       // V^T, written after the inverse
-    } u;
-    float T[kChunk * kMatStride];
-    float c[kChunk];     // in-chunk cumsum of g
-    float b[kChunk];     // beta
-    float be[kChunk];    // beta * e^c
-    float ed[kChunk];    // e^{c_63 - c}
-    float es[kChunk];    // s * e^c
-    int red[kPrepThreads];
+    uint16_t Kr[kChunk * kKS];   // K rows (bf16, as loaded), [token][dk]
+    _Float16 Vt[kDV * kTS];      // V^T (fp16), [dv][token]; first 1 KB doubles as scan scratch
+    // A (strictly lower, row-major) on entry.  The inverse overwrites it in
+    // place: diagonal blocks T_ii row-major at (i, i); T_ij (i > j) stored
+    // transposed at block (j, i), where A is zero and never read.
+    float AT[kChunk * kMS];
+    float cl[kChunk];   // c * log2(e)
+    float b[kChunk];    // beta
+    float be[kChunk];   // beta e^c
+    float ed[kChunk];   // e^{c_63 - c}
 };
 
-__global__ __launch_bounds__(kPrepThreads, 2) void gdn_prep_kernel(
+// T[r][c0 .. c0+3] (c0 a multiple of 4) from the in-place inverse layout.
+// Row block rb and column block cb are compile-time, so the branch is uniform.
+__device__ inline f32x4 t_row4(const float* AT, int rb, int cb, int r, int c0) {
+    if (cb == rb) return *reinterpret_cast<const f32x4*>(&AT[r * kMS + c0]);
+    if (cb > rb) return zero4();
+    f32x4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = AT[(c0 + e) * kMS + r];
+    return t;
+}
+
+__global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ g,
     const float* __restrict__ beta, const int32_t* __restrict__ cu, int N, int T, int HV,
-    int HK, float scale, Workspace ws) {
+    int HK, int nch_bound, float scale, Workspace ws) {
     __shared__ PrepSmem sm;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
-    const int cid = blockIdx.x, hv = blockIdx.y;
+
+    // Work-group id -> (chunk, k-head, member of its GQA group).  The rep
+    // v-heads that read one k-head get ids 8 apart, i.e. the same XCD
+    // (work-group i runs on XCD i % 8), so their q / k rows come from one L2.
+    const int rep = HV / HK;
+    const int L = blockIdx.x;
+    const int rest = L >> 3;
+    const int z = (rest / rep) * 8 + (L & 7);
+    const int cid = z / HK, hk = z - cid * HK;
+    if (cid >= nch_bound) return;
+    const int hv = hk * rep + (rest % rep);
 
     int seq, tok0, rows;
-    if (!locate_chunk<kPrepThreads>(cu, N, T, cid, sm.red, seq, tok0, rows)) return;
-    const int hk = hv / (HV / HK);
+    if (!locate_chunk<kPrepThreads>(cu, N, T, cid, reinterpret_cast<int*>(sm.Vt), seq, tok0,
+                                    rows))
+        return;
     const size_t ch = (size_t)cid * HV + hv;
 
-    // ---- issue global loads: K (to LDS), V (kept in registers), Q fragments
-    uint4 vraw[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int e = tid + it * kPrepThreads;  // 16-byte piece of the 64x128 tile
-        const int r = e >> 4, c8 = (e & 15) * 8;
-        uint4 kr = {0u, 0u, 0u, 0u}, vr = {0u, 0u, 0u, 0u};
-        if (r < rows) {
-            kr = *reinterpret_cast<const uint4*>(k + ((size_t)(tok0 + r) * HK + hk) * kDK + c8);
-            vr = *reinterpret_cast<const uint4*>(v + ((size_t)(tok0 + r) * HV + hv) * kDV + c8);
-        }
-        vraw[it] = vr;
-        const half8 kh = bf16x8_to_half8(kr);
-        *reinterpret_cast<half8*>(&sm.Kr[r * kKrStride + c8]) = kh;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sm.Kt[(c8 + j) * kKtStride + r] = kh[j];
-    }
-    // Q rows of this wave's 16-row block, as B/A fragments for the 4 k-blocks
-    half8 qf[4];
+    // ---- global loads, all issued before any is consumed.  Rows past the
+    // chunk's end read the last valid row (always in bounds) and are zeroed
+    // afterwards, so no load sits behind a branch.
+    // Threads 0..127 copy K rows (16-byte pieces, row-major, bf16) to LDS;
+    // threads 128..255 own an 8-row x 8-column block of V for the transpose.
+    const bool kthr = wave < 2;   // wave-uniform
+    const int blk = tid & 127, rg = blk & 7, cc = blk >> 3;
+    u32x4 raw[8];
     {
-        const int r = wave * 16 + lm;
+        // K piece ii: row (blk + 128 ii) / 16, columns 8 * (blk % 16) ..;
+        // V piece ii: row 8 rg + ii, columns 8 cc ..
+        const uint16_t* base = kthr ? k + ((size_t)tok0 * HK + hk) * kDK + 8 * (blk & 15)
+                                    : v + ((size_t)tok0 * HV + hv) * kDV + 8 * cc;
+        const size_t pitch = (size_t)(kthr ? HK : HV) * kDK;
+        const int r0 = kthr ? (blk >> 4) : 8 * rg;
+        const int rstep = kthr ? 8 : 1;
+#pragma unroll
+        for (int ii = 0; ii < 8; ++ii) {
+            const int r = min(r0 + rstep * ii, rows - 1);
+            raw[ii] = *reinterpret_cast<const u32x4*>(base + (size_t)r * pitch);
+        }
+    }
+    // this wave's Q rows (k-map over dk); bf16 straight into the MFMA
+    uint2 qr[4][2];
+    {
+        const uint16_t* qs =
+            q + ((size_t)(tok0 + min(wave * 16 + lm, rows - 1)) * HK + hk) * kDK + 4 * lg;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            uint2 lo = {0u, 0u}, hi = {0u, 0u};
-            if (r < rows) {
-                const uint16_t* src = q + ((size_t)(tok0 + r) * HK + hk) * kDK + kb * 32 + 4 * lg;
-                lo = *reinterpret_cast<const uint2*>(src);
-                hi = *reinterpret_cast<const uint2*>(src + 16);
-            }
-            qf[kb] = cat8(bf16x4_to_half4(lo), bf16x4_to_half4(hi));
+            qr[kb][0] = *reinterpret_cast<const uint2*>(qs + kb * 32);
+            qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
         }
     }
-    // gates: wave 0 scans g over the 64 rows
+    float gv = 0.f, bv = 0.f;
     if (wave == 0) {
-        const bool valid = lane < rows;
-        const float gv = valid ? g[(size_t)(tok0 + lane) * HV + hv] : 0.f;
-        const float bv = valid ? beta[(size_t)(tok0 + lane) * HV + hv] : 0.f;
+        const int r = min(lane, rows - 1);
+        gv = g[(size_t)(tok0 + r) * HV + hv];
+        bv = beta[(size_t)(tok0 + r) * HV + hv];
+    }
+
+    // ---- gates (wave 0): c = cumsum(g); padded rows have g = beta = 0
+    if (wave == 0) {
+        if (lane >= rows) {
+            gv = 0.f;
+            bv = 0.f;
+        }
         float cs = gv;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -258,62 +303,111 @@ __global__ __launch_bounds__(kPrepThreads, 2) void gdn_prep_kernel(
             if (lane >= off) cs += o;
         }
         const float clast = __shfl(cs, 63, 64);
-        const float ec = expf(cs);
-        sm.c[lane] = cs;
+        const float c2 = cs * kLog2e;
+        const float ec = exp2f(c2);
+        sm.cl[lane] = c2;
         sm.b[lane] = bv;
         sm.be[lane] = bv * ec;
-        sm.ed[lane] = expf(clast - cs);
-        sm.es[lane] = scale * ec;
-        if (lane == 0) ws.decay[ch] = expf(clast);
+        sm.ed[lane] = exp2f((clast - cs) * kLog2e);
+        float* gr = ws.gates + ch * kGateFloats;
+        gr[lane] = scale * ec;
+        if (lane == 0) gr[kGateDecay] = exp2f(clast * kLog2e);
         if (ws.dbgC) ws.dbgC[ch * kChunk + lane] = cs;
+    }
+
+    // ---- K rows -> LDS as loaded; V block -> 8x8 register transpose -> V^T (fp16)
+    {
+        // rows past the chunk's end are zeroed (padding rows contribute nothing)
+        if (kthr) {
+#pragma unroll
+            for (int ii = 0; ii < 8; ++ii) {
+                const int r = (blk >> 4) + 8 * ii;
+                const uint32_t m = r < rows ? 0xffffffffu : 0u;
+                *reinterpret_cast<u32x4*>(&sm.Kr[r * kKS + 8 * (blk & 15)]) = raw[ii] & m;
+            }
+        } else {
+            half8 hrow[8];
+#pragma unroll
+            for (int ii = 0; ii < 8; ++ii) {
+                const uint32_t m = 8 * rg + ii < rows ? 0xffffffffu : 0u;
+                const u32x4 w = raw[ii] & m;
+                const uint4 w4 = {w[0], w[1], w[2], w[3]};
+                hrow[ii] = bf16x8_to_half8(w4);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                half4 lo, hi;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lo[e] = hrow[e][jj];
+                    hi[e] = hrow[4 + e][jj];
+                }
+                half4* dst = reinterpret_cast<half4*>(&sm.Vt[(8 * cc + jj) * kTS + 8 * rg]);
+                dst[0] = lo;
+                dst[1] = hi;
+            }
+        }
     }
     __syncthreads();
 
     // ---- A = -beta_r (k_r . k_j) Gamma_rj (r > j) and M = s (q_r . k_j) Gamma_rj (r >= j)
-    // wave w owns column block j in [16w, 16w+16) of A and query-row block
+    // Wave w owns column block j in [16w, 16w+16) of A and query-row block
     // r in [16w, 16w+16) of M (computed as M^T = K Q^T so the accumulator is
     // already in A-fragment order for the scan).
     {
-        half8 kb_w[4];  // K rows of block w as B operand (B[k][n] = K[16w+n][k])
+        const uint2 z2 = {0u, 0u};
+        bf16x8 ka[4][4], kw[4], qf[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const uint16_t* src = &sm.Kr[(mt * 16 + lm) * kKS + 4 * lg];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                ka[mt][kb] = bf16_frag(*reinterpret_cast<const uint2*>(src + kb * 32),
+                                       *reinterpret_cast<const uint2*>(src + kb * 32 + 16));
+        }
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const _Float16* src = &sm.Kr[(wave * 16 + lm) * kKrStride + kb * 32 + 4 * lg];
-            kb_w[kb] = cat8(*reinterpret_cast<const half4*>(src),
-                            *reinterpret_cast<const half4*>(src + 16));
+            kw[kb] = ka[0][kb];
+#pragma unroll
+            for (int mt = 1; mt < 4; ++mt)
+                if (mt == wave) kw[kb] = ka[mt][kb];
+        }
+        {
+            const bool ok = wave * 16 + lm < rows;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                qf[kb] = bf16_frag(ok ? qr[kb][0] : z2, ok ? qr[kb][1] : z2);
         }
         f32x4 accA[4], accM[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             accA[mt] = zero4();
             accM[mt] = zero4();
-            if (mt >= wave || mt <= wave) {
+            if (mt >= wave) {
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    const _Float16* src = &sm.Kr[(mt * 16 + lm) * kKrStride + kb * 32 + 4 * lg];
-                    const half8 a = cat8(*reinterpret_cast<const half4*>(src),
-                                         *reinterpret_cast<const half4*>(src + 16));
-                    if (mt >= wave) accA[mt] = mfma16(a, kb_w[kb], accA[mt]);
-                    if (mt <= wave) accM[mt] = mfma16(a, qf[kb], accM[mt]);
-                }
+                for (int kb = 0; kb < 4; ++kb) accA[mt] = mfma16_bf16(ka[mt][kb], kw[kb], accA[mt]);
+            }
+            if (mt <= wave) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) accM[mt] = mfma16_bf16(ka[mt][kb], qf[kb], accM[mt]);
             }
         }
-        // A: element (r = 16mt + 4lg + i, col = 16w + lm)
+        // A: element (r = 16mt + 4lg + i, col = 16w + lm); the upper part of
+        // column block w is written as zero
         const int col = wave * 16 + lm;
-        const float ccol = sm.c[col];
+        const float ccol = sm.cl[col];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = mt * 16 + 4 * lg + i;
                 float a = 0.f;
-                if (r > col) a = -sm.b[r] * accA[mt][i] * expf(sm.c[r] - ccol);
-                sm.u.A[r * kMatStride + col] = a;
+                if (r > col) a = -sm.b[r] * accA[mt][i] * exp2f(sm.cl[r] - ccol);
+                sm.AT[r * kMS + col] = a;
                 if (ws.dbgA) ws.dbgA[ch * kChunk * kChunk + r * kChunk + col] = a;
             }
         }
-        // M^T tile (mt, w): element (key c = 16mt + 4lg + i, query r = 16w + lm)
-        const int rq = wave * 16 + lm;
-        const float crq = sm.c[rq];
+        // M^T tile (mt, w): element (key ck = 16mt + 4lg + i, query col)
         half4 mh[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
@@ -321,204 +415,18 @@ __global__ __launch_bounds__(kPrepThreads, 2) void gdn_prep_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int ck = mt * 16 + 4 * lg + i;
-                val[i] = (ck <= rq) ? scale * accM[mt][i] * expf(crq - sm.c[ck]) : 0.f;
+                val[i] = (ck <= col) ? scale * accM[mt][i] * exp2f(ccol - sm.cl[ck]) : 0.f;
             }
             mh[mt] = to_half4(val);
         }
-        // Mf fragment (row block w, k-block kbm) = tiles 2kbm, 2kbm+1
         half8* mdst = reinterpret_cast<half8*>(ws.Mf + ch * kMfElems);
         mdst[(wave * 2 + 0) * 64 + lane] = cat8(mh[0], mh[1]);
         mdst[(wave * 2 + 1) * 64 + lane] = cat8(mh[2], mh[3]);
-        // Qf fragments: s e^{c_r} q_r, row block w
-        const float es = sm.es[rq];
-        half8* qdst = reinterpret_cast<half8*>(ws.Qf + ch * kQfElems);
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            half8 o;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = (_Float16)((float)qf[kb][j] * es);
-            qdst[(wave * 4 + kb) * 64 + lane] = o;
-        }
     }
-    __syncthreads();
-
-    // ---- T = (I - A)^-1 in fp32: 16x16 diagonal blocks by forward
-    // substitution (wave w owns block w, lanes 0..15 own its columns), then
-    // the off-diagonal blocks level by level:
-    //   T_ij = T_ii * sum_{k=j}^{i-1} A_ik T_kj
-    if (lm == lane) {  // lanes 0..15 of every wave
-        const int b0 = wave * 16;
-        const int cidx = lm;
-        float col[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) col[i] = (i == cidx) ? 1.f : 0.f;
-#pragma unroll
-        for (int i = 1; i < 16; ++i) {
-            const float* arow = &sm.u.A[(b0 + i) * kMatStride + b0];
-            float s = 0.f;
-#pragma unroll
-            for (int j = 0; j < i; ++j) s = fmaf(arow[j], col[j], s);
-            if (i > cidx) col[i] = s;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sm.T[(b0 + i) * kMatStride + b0 + cidx] = col[i];
-    }
-    // zero the strictly upper blocks of T
-    for (int e = tid; e < 6 * 256; e += kPrepThreads) {
-        const int blk = e >> 8, w = e & 255;
-        // upper block pairs (i < j): (0,1)(0,2)(0,3)(1,2)(1,3)(2,3)
-        const int bi = (blk < 3) ? 0 : (blk < 5 ? 1 : 2);
-        const int bj = (blk < 3) ? blk + 1 : (blk < 5 ? blk - 1 : 3);
-        sm.T[(bi * 16 + (w >> 4)) * kMatStride + bj * 16 + (w & 15)] = 0.f;
-    }
-    __syncthreads();
-    // levels d = 1..3: blocks (j + d, j) for j = 0 .. 3-d
-#pragma unroll
-    for (int d = 1; d <= 3; ++d) {
-        const int nblk = 4 - d;
-        // P_ij = sum_{k=j}^{i-1} A_ik T_kj  -> registers
-        float pv[3];
-#pragma unroll
-        for (int it = 0; it < 3; ++it) {
-            const int e = tid + it * kPrepThreads;
-            pv[it] = 0.f;
-            if (e < nblk * 256) {
-                const int j = e >> 8, i = j + d;
-                const int r = (e >> 4) & 15, cc = e & 15;
-                float s = 0.f;
-                for (int kk = j * 16; kk < i * 16; ++kk)
-                    s = fmaf(sm.u.A[(i * 16 + r) * kMatStride + kk], sm.T[kk * kMatStride + j * 16 + cc], s);
-                pv[it] = s;
-            }
-        }
-        __syncthreads();
-        // stash P in the (still zero) target block of T
-#pragma unroll
-        for (int it = 0; it < 3; ++it) {
-            const int e = tid + it * kPrepThreads;
-            if (e < nblk * 256) {
-                const int j = e >> 8, i = j + d;
-                const int r = (e >> 4) & 15, cc = e & 15;
-                sm.T[(i * 16 + r) * kMatStride + j * 16 + cc] = pv[it];
-            }
-        }
-        __syncthreads();
-        // T_ij = T_ii P_ij
-#pragma unroll
-        for (int it = 0; it < 3; ++it) {
-            const int e = tid + it * kPrepThreads;
-            pv[it] = 0.f;
-            if (e < nblk * 256) {
-                const int j = e >> 8, i = j + d;
-                const int r = (e >> 4) & 15, cc = e & 15;
-                float s = 0.f;
-#pragma unroll
-                for (int kk = 0; kk < 16; ++kk)
-                    s = fmaf(sm.T[(i * 16 + r) * kMatStride + i * 16 + kk],
-                             sm.T[(i * 16 + kk) * kMatStride + j * 16 + cc], s);
-                pv[it] = s;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < 3; ++it) {
-            const int e = tid + it * kPrepThreads;
-            if (e < nblk * 256) {
-                const int j = e >> 8, i = j + d;
-                const int r = (e >> 4) & 15, cc = e & 15;
-                sm.T[(i * 16 + r) * kMatStride + j * 16 + cc] = pv[it];
-            }
-        }
-        __syncthreads();
-    }
-    if (ws.dbgT) {
-        for (int e = tid; e < kChunk * kChunk; e += kPrepThreads)
-            ws.dbgT[ch * kChunk * kChunk + e] = sm.T[(e >> 6) * kMatStride + (e & 63)];
-    }
-    // ---- V^T into LDS (A is dead now)
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int e = tid + it * kPrepThreads;
-        const int r = e >> 4, c8 = (e & 15) * 8;
-        const half8 vh = bf16x8_to_half8(vraw[it]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sm.u.Vt[(c8 + j) * kKtStride + r] = vh[j];
-    }
-    __syncthreads();
-
-    // ---- U = (T diag(beta)) V : tiles (mt 0..3) x (nt = 2w, 2w+1)
-    {
-        half8 xa[4][2];  // A fragments of T diag(beta)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int r = mt * 16 + lm;
-                const int k0 = kb * 32 + 4 * lg;
-                const f32x4 t0 = *reinterpret_cast<const f32x4*>(&sm.T[r * kMatStride + k0]);
-                const f32x4 t1 = *reinterpret_cast<const f32x4*>(&sm.T[r * kMatStride + k0 + 16]);
-                const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sm.b[k0]);
-                const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sm.b[k0 + 16]);
-                xa[mt][kb] = cat8(to_half4(t0 * b0), to_half4(t1 * b1));
-            }
-        }
-        f32x4* udst = reinterpret_cast<f32x4*>(ws.Uf + ch * kUfElems);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int nt = wave * 2 + p;
-            half8 vb[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const _Float16* src = &sm.u.Vt[(nt * 16 + lm) * kKtStride + kb * 32 + 4 * lg];
-                vb[kb] = cat8(*reinterpret_cast<const half4*>(src),
-                              *reinterpret_cast<const half4*>(src + 16));
-            }
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                f32x4 acc = zero4();
-                acc = mfma16(xa[mt][0], vb[0], acc);
-                acc = mfma16(xa[mt][1], vb[1], acc);
-                udst[(nt * 4 + mt) * 64 + lane] = acc;  // slice nt, row tile mt
-            }
-        }
-    }
-    // ---- W^T = K^T (T diag(beta e^c))^T : tiles (dk mt = 2w, 2w+1) x (token nt 0..3)
-    {
-        half8 ka[2][2];
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int mt = wave * 2 + p;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const _Float16* src = &sm.Kt[(mt * 16 + lm) * kKtStride + kb * 32 + 4 * lg];
-                ka[p][kb] = cat8(*reinterpret_cast<const half4*>(src),
-                                 *reinterpret_cast<const half4*>(src + 16));
-            }
-        }
-        half8* wdst = reinterpret_cast<half8*>(ws.Wf + ch * kWfElems);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-            half8 xb[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int r = nt * 16 + lm;
-                const int k0 = kb * 32 + 4 * lg;
-                const f32x4 t0 = *reinterpret_cast<const f32x4*>(&sm.T[r * kMatStride + k0]);
-                const f32x4 t1 = *reinterpret_cast<const f32x4*>(&sm.T[r * kMatStride + k0 + 16]);
-                const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sm.be[k0]);
-                const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sm.be[k0 + 16]);
-                xb[kb] = cat8(to_half4(t0 * b0), to_half4(t1 * b1));
-            }
-            f32x4 acc0 = zero4(), acc1 = zero4();
-            acc0 = mfma16(ka[0][0], xb[0], acc0);
-            acc0 = mfma16(ka[0][1], xb[1], acc0);
-            acc1 = mfma16(ka[1][0], xb[0], acc1);
-            acc1 = mfma16(ka[1][1], xb[1], acc1);
-            // W fragment (row tile nt, k-block w): regs 0..3 = dk tile 2w, 4..7 = 2w+1
-            wdst[(nt * 4 + wave) * 64 + lane] = cat8(to_half4(acc0), to_half4(acc1));
-        }
-    }
-    // ---- K~^T fragments: e^{c_63 - c_tau} k_tau[dk], dk tiles 2w, 2w+1
+    // ---- K^T fragments (dk tiles 2w, 2w+1; k-map over tokens), gathered
+    // from the K rows in LDS: kt (unscaled) for W^T below, and the decayed
+    // e^{c_63 - c_tau} k_tau[dk] fragments the scan streams.
+    half8 kt[2][2];
     {
         half8* kdst = reinterpret_cast<half8*>(ws.Kf + ch * kKfElems);
 #pragma unroll
@@ -527,99 +435,272 @@ __global__ __launch_bounds__(kPrepThreads, 2) void gdn_prep_kernel(
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const int k0 = kb * 32 + 4 * lg;
-                const _Float16* src = &sm.Kt[(mt * 16 + lm) * kKtStride + k0];
-                const half4 lo = *reinterpret_cast<const half4*>(src);
-                const half4 hi = *reinterpret_cast<const half4*>(src + 16);
+                const uint16_t* src = &sm.Kr[k0 * kKS + mt * 16 + lm];
                 const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.ed[k0]);
                 const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.ed[k0 + 16]);
-                f32x4 l, h;
+                f32x4 klo, khi;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    l[j] = (float)lo[j] * d0[j];
-                    h[j] = (float)hi[j] * d1[j];
+                    klo[j] = bf16_bits_to_f32(src[j * kKS]);
+                    khi[j] = bf16_bits_to_f32(src[(16 + j) * kKS]);
                 }
-                kdst[(mt * 2 + kb) * 64 + lane] = cat8(to_half4(l), to_half4(h));
+                kt[p][kb] = cat8(to_half4(klo), to_half4(khi));
+                kdst[(mt * 2 + kb) * 64 + lane] = cat8(to_half4(klo * d0), to_half4(khi * d1));
             }
+        }
+    }
+    __syncthreads();
+
+    // ---- T = (I - A)^-1 in fp32, in place in AT
+    // (1) 16x16 diagonal blocks by forward substitution: wave 0, lane =
+    //     16 * block + column; T[i][c] = sum_{j<i} A[i][j] T[j][c] for i > c,
+    //     T[c][c] = 1, T[i][c] = 0 for i < c.  Each lane keeps its column in
+    //     registers and writes it after every row of the block was read.
+    if (wave == 0) {
+        const int b0 = lg * 16, cidx = lm;
+        float col[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) col[i] = (i == cidx) ? 1.f : 0.f;
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+            const float* arow = &sm.AT[(b0 + i) * kMS + b0];
+            float s = 0.f;
+#pragma unroll
+            for (int j4 = 0; j4 < (i + 3) / 4; ++j4) {
+                const f32x4 a4 = *reinterpret_cast<const f32x4*>(arow + 4 * j4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * j4 + e < i) s = fmaf(a4[e], col[4 * j4 + e], s);
+            }
+            if (i > cidx) col[i] = s;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sm.AT[(b0 + i) * kMS + b0 + cidx] = col[i];
+    }
+    __syncthreads();
+    // (2) off-diagonal blocks level by level, block (i, j) with i - j = d:
+    //     T_ij = T_ii * sum_{kk=j}^{i-1} A_{i,kk} T_{kk,j}
+    //     on fp32 MFMA 16x16x4 with k = 4 * lane group + s, so the A operand
+    //     is one 16-byte row read and a D-layout accumulator is directly the
+    //     B operand of the next product.  Wave w takes block (w + d, w).
+#pragma unroll
+    for (int d = 1; d <= 3; ++d) {
+        if (wave < 4 - d) {
+            const int j = wave, i = wave + d;
+            f32x4 P = zero4();
+#pragma unroll
+            for (int kk = j; kk < i; ++kk) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * i + lm) * kMS + 16 * kk + 4 * lg]);
+                f32x4 bt;
+                if (kk == j) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) bt[s] = sm.AT[(16 * j + 4 * lg + s) * kMS + 16 * j + lm];
+                } else {
+                    bt = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * j + lm) * kMS + 16 * kk + 4 * lg]);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) P = mfma_f32_16x16x4(a[s], bt[s], P);
+            }
+            const f32x4 t = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * i + lm) * kMS + 16 * i + 4 * lg]);
+            f32x4 R = zero4();
+#pragma unroll
+            for (int s = 0; s < 4; ++s) R = mfma_f32_16x16x4(t[s], P[s], R);
+            // R[s] = T_ij[4lg + s][lm] -> transposed slot (j, i)
+            *reinterpret_cast<f32x4*>(&sm.AT[(16 * j + lm) * kMS + 16 * i + 4 * lg]) = R;
+        }
+        __syncthreads();
+    }
+    if (ws.dbgT) {
+        for (int e = tid; e < kChunk * kChunk; e += kPrepThreads) {
+            const int r = e >> 6, c = e & 63;
+            float t = 0.f;
+            if ((r >> 4) == (c >> 4)) t = sm.AT[r * kMS + c];
+            else if (r > c) t = sm.AT[c * kMS + r];
+            ws.dbgT[ch * kChunk * kChunk + e] = t;
+        }
+    }
+
+    // ---- T fragments (rows 16mt + lm, k-map over tokens), scaled by beta
+    // (U = T diag(beta) V) and by beta e^c (W = T diag(beta e^c) K).
+    half8 xa[4][2], xb[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int r = mt * 16 + lm;
+            const int k0 = kb * 32 + 4 * lg;
+            const f32x4 t0 = t_row4(sm.AT, mt, 2 * kb, r, k0);
+            const f32x4 t1 = t_row4(sm.AT, mt, 2 * kb + 1, r, k0 + 16);
+            const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sm.b[k0]);
+            const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sm.b[k0 + 16]);
+            const f32x4 e0 = *reinterpret_cast<const f32x4*>(&sm.be[k0]);
+            const f32x4 e1 = *reinterpret_cast<const f32x4*>(&sm.be[k0 + 16]);
+            xa[mt][kb] = cat8(to_half4(t0 * b0), to_half4(t1 * b1));
+            xb[mt][kb] = cat8(to_half4(t0 * e0), to_half4(t1 * e1));
+        }
+    }
+    // ---- U = (T diag(beta)) V: slices nt = 2w, 2w+1, all four row tiles.
+    // T is lower triangular: row tiles 0 and 1 see only tokens 0..31.
+    {
+        half8* udst = reinterpret_cast<half8*>(ws.Uf + ch * kUfElems);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int nt = wave * 2 + p;
+            half8 vb[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const _Float16* src = &sm.Vt[(nt * 16 + lm) * kTS + kb * 32 + 4 * lg];
+                vb[kb] = cat8(*reinterpret_cast<const half4*>(src),
+                              *reinterpret_cast<const half4*>(src + 16));
+            }
+            half4 uh[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                f32x4 acc = mfma16(xa[mt][0], vb[0], zero4());
+                if (mt >= 2) acc = mfma16(xa[mt][1], vb[1], acc);
+                uh[mt] = to_half4(acc);
+            }
+            udst[(nt * 2 + 0) * 64 + lane] = cat8(uh[0], uh[1]);
+            udst[(nt * 2 + 1) * 64 + lane] = cat8(uh[2], uh[3]);
+        }
+    }
+    // ---- W^T = K^T (T diag(beta e^c))^T: dk tiles 2w, 2w+1 x token tiles nt.
+    // The D layout of W^T tiles (2w, 2w+1) is W's A fragment (nt, k-block w).
+    {
+        half8* wdst = reinterpret_cast<half8*>(ws.Wf + ch * kWfElems);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            f32x4 acc0 = mfma16(kt[0][0], xb[nt][0], zero4());
+            f32x4 acc1 = mfma16(kt[1][0], xb[nt][0], zero4());
+            if (nt >= 2) {
+                acc0 = mfma16(kt[0][1], xb[nt][1], acc0);
+                acc1 = mfma16(kt[1][1], xb[nt][1], acc1);
+            }
+            wdst[(nt * 4 + wave) * 64 + lane] = cat8(to_half4(acc0), to_half4(acc1));
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (2 waves) per (state slice, v-head, sequence)
+// scan kernel: one work-group (8 waves) per (state slice, v-head, sequence)
+//
+//   wave 0      the chain: keeps its 128x16 fp32 state slice in registers and
+//               per chunk forms V_n = U - W S and S <- e^{c_63} S + K~^T V_n,
+//               reading W, K~^T, U and the decay from a 3-stage LDS ring.
+//               It also warms L2 kWarmAhead chunks ahead: two strided
+//               LDS-direct loads per chunk touch this slice's eighth of the
+//               lines of W, K~^T, M and q and all of its U, so the eight
+//               slices of a head cover each line once and the loaders and
+//               output waves find their data in L2.
+//   waves 4-6   loaders: each moves a third of a chunk's chain operands
+//               (fragment-ordered, 16 bytes per lane per fragment) from
+//               L2 / HBM into the ring up to two chunks ahead of the chain.
+//   waves 1-3, 7   four output waves; the j-th forms O for chunks c = j mod 4
+//               from S_c and V_n handed over in LDS slot j.
+// Waves meet only through LDS counters with bounded waits, never through a
+// work-group barrier, so no wave waits on a slower one it does not need.
 // ---------------------------------------------------------------------------
+constexpr int kRing = 3;               // operand stages
+constexpr int kHand = 4;               // hand-off slots: chunk c uses slot c % kHand
+constexpr int kLoaders = 3;
+constexpr int kWarmAhead = 8;          // chunks between the chain and the L2 warm-up
+constexpr int kSpinLimit = 1 << 20;    // bounded waits: ~0.1 s, then the wave gives up
+static_assert(kOutWaves == kHand, "output wave j owns hand-off slot j");
+
+// The 34 fragments of one chain step (16 of W, 16 of K~^T, 2 of U), split
+// over the loaders: fragment f lives at LDS fragment index f of a stage.
+constexpr int kStageFrags = 34;
+constexpr int kLoaderFrags[kLoaders + 1] = {0, 12, 24, 34};
+
 struct ScanSmem {
-    half8 ringS[2][4][64];   // S as B-operand fragments (4 k-blocks over dk)
-    half8 ringV[2][2][64];   // V_new as B-operand fragments (2 k-blocks over tokens)
+    half8 stage[kRing][kStageFrags][64];   // [stage][W 0..15 | K~^T 16..31 | U 32..33][lane]
+    float gd[kRing];                        // e^{c_63} of the chunk in each stage
+    half8 hs[kHand][4][64];                 // S at the start of a chunk, B-fragments
+    half8 hv[kHand][2][64];                 // V_n, B-fragments
+    uint32_t warm[256];                     // landing area of the L2 warm-up loads (never read)
+    int filled[kLoaders];                   // per loader: chunks whose part sits in the ring
+    int freed;                              // chunks whose stage the chain has finished reading
+    int ready;                              // chunks whose S / V_n sit in the hand-off slots
+    int cons[kHand];                        // per slot: 1 + the chunk an output wave last read from it
     int red[kScanThreads / 64];
 };
 
-struct ChainOps {
-    half8 w[16];
-    half8 k[16];
-    f32x4 u[4];
-    float d;
-};
-
-__device__ inline void load_chain(const Workspace& ws, size_t ch, int sl, int lane, ChainOps& op) {
-    const half8* wsrc = reinterpret_cast<const half8*>(ws.Wf + ch * kWfElems);
-    const half8* ksrc = reinterpret_cast<const half8*>(ws.Kf + ch * kKfElems);
-    const f32x4* usrc = reinterpret_cast<const f32x4*>(ws.Uf + ch * kUfElems);
-#pragma unroll
-    for (int f = 0; f < 16; ++f) op.w[f] = wsrc[f * 64 + lane];
-#pragma unroll
-    for (int f = 0; f < 16; ++f) op.k[f] = ksrc[f * 64 + lane];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) op.u[mt] = usrc[(sl * 4 + mt) * 64 + lane];
-    op.d = ws.decay[ch];
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-struct OutOps {
-    half8 q[16];
-    half8 m[8];
-};
-
-__device__ inline void load_out(const Workspace& ws, size_t ch, int lane, OutOps& op) {
-    const half8* qsrc = reinterpret_cast<const half8*>(ws.Qf + ch * kQfElems);
-    const half8* msrc = reinterpret_cast<const half8*>(ws.Mf + ch * kMfElems);
-#pragma unroll
-    for (int f = 0; f < 16; ++f) op.q[f] = qsrc[f * 64 + lane];
-#pragma unroll
-    for (int f = 0; f < 8; ++f) op.m[f] = msrc[f * 64 + lane];
+// LDS-direct loads, issued from assembly so the compiler's wait-count pass
+// does not see them; the caller waits with vmcnt explicitly.  With M0 = LDS
+// byte address `lds` and global address `sbase + voff`, lane l's 16 bytes of
+// the transfer with immediate offset X come from sbase + voff_l + X and land
+// at lds + X + 16 * l (the offset applies to both sides).  voff_l = 16 * l
+// makes each transfer one contiguous 1 KB fragment.
+__device__ __forceinline__ void dma16x4(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:1024\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:2048\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:3072"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds)
+        : "memory", "m0");
 }
 
-__device__ inline void chain_step(const ChainOps& op, f32x4 (&S)[8], half8 (&sb)[4], half8 (&vb)[2]) {
-    // P = W S  (64 x 16), k over dk
-    f32x4 P[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        P[mt] = zero4();
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) P[mt] = mfma16(op.w[mt * 4 + kb], sb[kb], P[mt]);
+__device__ __forceinline__ void dma16x2(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:1024"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds)
+        : "memory", "m0");
+}
+
+// 4 bytes per lane: lane l's word from sbase + voff_l lands at lds + 4 * l.
+__device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %0, %1"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds)
+        : "memory", "m0");
+}
+
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int lds_load_relaxed(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void lds_store_relaxed(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wait (bounded) until *flag >= target; false when the bound ran out.
+__device__ inline bool wait_ge(const int* flag, int target) {
+    for (int it = 0; it < kSpinLimit; ++it) {
+        if (lds_load_relaxed(flag) >= target) return true;
+        __builtin_amdgcn_s_sleep(1);
     }
-    // V_new = U - P
-    f32x4 vn[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) vn[mt] = op.u[mt] - P[mt];
-    vb[0] = cat8(to_half4(vn[0]), to_half4(vn[1]));
-    vb[1] = cat8(to_half4(vn[2]), to_half4(vn[3]));
-    // S = d S + K~^T V_new   (128 x 16), k over tokens
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        f32x4 acc = S[t] * op.d;
-        acc = mfma16(op.k[t * 2 + 0], vb[0], acc);
-        acc = mfma16(op.k[t * 2 + 1], vb[1], acc);
-        S[t] = acc;
-    }
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
+    return false;
 }
 
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
-    Workspace ws, uint16_t* __restrict__ o, const float* __restrict__ s0,
-    float* __restrict__ sf, const int32_t* __restrict__ cu, int N, int T, int HV) {
+    Workspace ws, const uint16_t* __restrict__ q, uint16_t* __restrict__ o,
+    const float* __restrict__ s0, float* __restrict__ sf, const int32_t* __restrict__ cu, int N,
+    int T, int HV, int HK) {
     __shared__ ScanSmem sm;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
 
     // XCD-aware id: the 8 slices of one (seq, head) pair share id % 8
@@ -629,75 +710,241 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     const int pair = (qd >> 3) * 8 + xcd;
     if (pair >= N * HV) return;
     const int seq = pair / HV, hv = pair - seq * HV;
+    const int hk = hv / (HV / HK);
 
     const int len = seq_len(cu, T, seq);
     const int tok0 = seq_start(cu, T, seq);
     const int nch = (len + kChunk - 1) / kChunk;
-    const int chunk0 = chunks_before<kScanThreads>(cu, T, seq, sm.red);
-    const size_t sbase = ((size_t)seq * HV + hv) * kDK * kDV + sl * kBV + lm;
+    const int chunk0 = __builtin_amdgcn_readfirstlane(chunks_before<kScanThreads>(cu, T, seq, sm.red));
+    if (tid < kLoaders) lds_store_relaxed(&sm.filled[tid], 0);
+    if (tid == 0) {
+        lds_store_relaxed(&sm.freed, 0);
+        lds_store_relaxed(&sm.ready, 0);
+    }
+    if (tid < kHand) lds_store_relaxed(&sm.cons[tid], 0);
+    __syncthreads();
 
     if (wave == 0) {
-        // ---- chain wave
+        // ---------------- chain wave
+        const size_t sbase = ((size_t)seq * HV + hv) * kDK * kDV + sl * kBV + lm;
         f32x4 S[8];
+        if (s0) {   // one uniform branch: all 32 loads in flight together
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+            for (int t = 0; t < 8; ++t) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                S[t][i] = s0 ? s0[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV] : 0.f;
+                for (int i = 0; i < 4; ++i) S[t][i] = s0[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) S[t] = zero4();
         }
-        half8 sb[4], vb[2];
+        half8 sb[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
-        ChainOps cur, nxt;
-        if (nch > 0) load_chain(ws, (size_t)chunk0 * HV + hv, sl, lane, cur);
-        for (int c = 0; c < nch; ++c) {
-            if (c + 1 < nch) load_chain(ws, (size_t)(chunk0 + c + 1) * HV + hv, sl, lane, nxt);
-            half8* rs = &sm.ringS[c & 1][0][0];
+
+        // L2 warm-up of chunk c: lane l touches one 128-byte line per load.
+        // First load: lanes 0-15 this slice's 2 KB of W, 16-31 of K~^T,
+        // 32-47 its U, 48-63 its 1 KB of M (twice).  Second load: q rows
+        // 8 sl .. 8 sl + 7 of the chunk (clamped to the sequence), 2 lines each.
+        const uint32_t lds_warm = __builtin_amdgcn_readfirstlane(lds_u32(&sm.warm[0]));
+        const int part = lane >> 4, li = lane & 15;
+        auto warm = [&](int c) {
+            const size_t chh = (size_t)(chunk0 + c) * HV + hv;
+            const char* a;
+            if (part == 0) a = reinterpret_cast<const char*>(ws.Wf + chh * kWfElems) + sl * 2048 + li * 128;
+            else if (part == 1) a = reinterpret_cast<const char*>(ws.Kf + chh * kKfElems) + sl * 2048 + li * 128;
+            else if (part == 2) a = reinterpret_cast<const char*>(ws.Uf + chh * kUfElems) + sl * 2048 + li * 128;
+            else a = reinterpret_cast<const char*>(ws.Mf + chh * kMfElems) + sl * 1024 + (li & 7) * 128;
+            const int r = min(c * kChunk + 8 * sl + ((lane >> 1) & 7), len - 1);
+            const char* b = reinterpret_cast<const char*>(q + ((size_t)(tok0 + r) * HK + hk) * kDK) + (lane & 1) * 128;
+            asm volatile(
+                "s_mov_b32 m0, %2\n\t"
+                "s_nop 0\n\t"
+                "global_load_lds_dwordx4 %0, off\n\t"
+                "global_load_lds_dwordx4 %1, off"
+                :
+                : "v"(a), "v"(b), "s"(lds_warm)
+                : "memory", "m0");
+        };
+        for (int c = 1; c < min(nch, kWarmAhead); ++c) warm(c);
+
+        bool ok = true;
+        int st = 0;      // stage of chunk c
+        int hslot = 0;   // hand-off slot of chunk c
+        for (int c = 0; c < nch && ok; ++c) {
+            if (c + kWarmAhead < nch) warm(c + kWarmAhead);
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) rs[kb * 64 + lane] = sb[kb];
-            chain_step(cur, S, sb, vb);
-            half8* rv = &sm.ringV[c & 1][0][0];
-            rv[0 * 64 + lane] = vb[0];
-            rv[1 * 64 + lane] = vb[1];
-            __syncthreads();
-            cur = nxt;
+            for (int j = 0; j < kLoaders; ++j) ok = ok && wait_ge(&sm.filled[j], c + 1);
+            asm volatile("" ::: "memory");
+            const half8(&sg)[kStageFrags][64] = sm.stage[st];
+            const float d = sm.gd[st];
+            half8 wv[16];
+#pragma unroll
+            for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
+            // P = W S (64 x 16), k over dk; the four row tiles are
+            // independent, so they are issued round-robin
+            f32x4 P[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4], sb[0], zero4());
+#pragma unroll
+            for (int kb = 1; kb < 4; ++kb) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4 + kb], sb[kb], P[mt]);
+            }
+            // independent of P: the decayed state and the K~^T operands
+#pragma unroll
+            for (int t = 0; t < 8; ++t) S[t] = S[t] * d;
+            half8 kv[16];
+#pragma unroll
+            for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
+            const half8 u0 = sg[32][lane], u1 = sg[33][lane];
+            // every read of this stage has landed: hand it back to the loaders
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) lds_store_relaxed(&sm.freed, c + 1);
+            // V_n = U - P
+            f32x4 vn[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vn[0][i] = (float)u0[i] - P[0][i];
+                vn[1][i] = (float)u0[4 + i] - P[1][i];
+                vn[2][i] = (float)u1[i] - P[2][i];
+                vn[3][i] = (float)u1[4 + i] - P[3][i];
+            }
+            half8 vb[2];
+            vb[0] = cat8(to_half4(vn[0]), to_half4(vn[1]));
+            vb[1] = cat8(to_half4(vn[2]), to_half4(vn[3]));
+            // S = d S + K~^T V_n (128 x 16), k over tokens; eight independent
+            // tiles, issued round-robin
+#pragma unroll
+            for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 0], vb[0], S[t]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 1], vb[1], S[t]);
+
+            // hand S_c (its fp16 copy sb) and V_n to the output waves while
+            // the products run
+            const int slot = hslot;
+            hslot = (hslot == kHand - 1) ? 0 : hslot + 1;
+            if (c >= kHand) ok = ok && wait_ge(&sm.cons[slot], c - kHand + 1);
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) sm.hs[slot][kb][lane] = sb[kb];
+            sm.hv[slot][0][lane] = vb[0];
+            sm.hv[slot][1][lane] = vb[1];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) lds_store_relaxed(&sm.ready, c + 1);
+
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
+            st = (st == kRing - 1) ? 0 : st + 1;
         }
+        // the warm-up loads land in LDS: drain them before the wave ends
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sf[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV] = S[t][i];
         }
-    } else {
-        // ---- output wave
-        OutOps cur, nxt;
-        if (nch > 0) load_out(ws, (size_t)chunk0 * HV + hv, lane, cur);
+    } else if (wave >= 4 && wave < 4 + kLoaders) {
+        // ---------------- loaders: chunk c into stage c % kRing once the
+        // chain has finished reading chunk c - kRing from it
+        const int j = wave - 4;
+        constexpr int kMaxFrags = 12;
+        const int f0 = kLoaderFrags[j], nf = kLoaderFrags[j + 1] - kLoaderFrags[j];
+        int st = 0;
         for (int c = 0; c < nch; ++c) {
-            if (c + 1 < nch) load_out(ws, (size_t)(chunk0 + c + 1) * HV + hv, lane, nxt);
-            __syncthreads();
-            half8 sb[4], vb[2];
-            const half8* rs = &sm.ringS[c & 1][0][0];
+            const size_t chh = (size_t)(chunk0 + c) * HV + hv;
+            const u32x4* wsrc = reinterpret_cast<const u32x4*>(ws.Wf + chh * kWfElems);
+            const u32x4* ksrc = reinterpret_cast<const u32x4*>(ws.Kf + chh * kKfElems);
+            const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sl * 2 * 64;
+            u32x4 frag[kMaxFrags];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) sb[kb] = rs[kb * 64 + lane];
-            const half8* rv = &sm.ringV[c & 1][0][0];
-            vb[0] = rv[lane];
-            vb[1] = rv[64 + lane];
+            for (int i = 0; i < kMaxFrags; ++i) {
+                const int f = f0 + min(i, nf - 1);
+                const u32x4* src = f < 16 ? wsrc + f * 64 : (f < 32 ? ksrc + (f - 16) * 64 : usrc + (f - 32) * 64);
+                frag[i] = src[lane];
+            }
+            const float dgt = (j == kLoaders - 1) ? ws.gates[chh * kGateFloats + kGateDecay] : 0.f;
+            if (c >= kRing && !wait_ge(&sm.freed, c - kRing + 1)) break;
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < kMaxFrags; ++i)
+                if (i < nf) *reinterpret_cast<u32x4*>(&sm.stage[st][f0 + i][lane]) = frag[i];
+            if (j == kLoaders - 1 && lane == 0) sm.gd[st] = dgt;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) lds_store_relaxed(&sm.filled[j], c + 1);
+            st = (st == kRing - 1) ? 0 : st + 1;
+        }
+    } else {
+        // ---------------- output waves: chunks c = ow, ow + kOutWaves, ...
+        const int ow = wave < 4 ? wave - 1 : 3;   // waves 1, 2, 3, 7
+        for (int c = ow; c < nch; c += kOutWaves) {
+            const size_t chh = (size_t)(chunk0 + c) * HV + hv;
             const int rows = min(kChunk, len - c * kChunk);
+            // operands of this chunk: raw q rows (k-map over dk), M, s e^c
+            uint2 qr[4][4][2];
+            const uint16_t* qb = q + ((size_t)(tok0 + c * kChunk) * HK + hk) * kDK + 4 * lg;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
-                f32x4 acc = zero4();
+                const uint16_t* src = qb + (size_t)min(mt * 16 + lm, rows - 1) * HK * kDK;
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) acc = mfma16(cur.q[mt * 4 + kb], sb[kb], acc);
-                acc = mfma16(cur.m[mt * 2 + 0], vb[0], acc);
-                acc = mfma16(cur.m[mt * 2 + 1], vb[1], acc);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = mt * 16 + 4 * lg + i;
-                    if (r < rows)
-                        o[((size_t)(tok0 + c * kChunk + r) * HV + hv) * kDV + sl * kBV + lm] =
-                            f32_to_bf16_bits(acc[i]);
+                for (int kb = 0; kb < 4; ++kb) {
+                    qr[mt][kb][0] = *reinterpret_cast<const uint2*>(src + kb * 32);
+                    qr[mt][kb][1] = *reinterpret_cast<const uint2*>(src + kb * 32 + 16);
                 }
             }
-            cur = nxt;
+            half8 mf[8];
+            const half8* msrc = reinterpret_cast<const half8*>(ws.Mf + chh * kMfElems);
+#pragma unroll
+            for (int f = 0; f < 8; ++f) mf[f] = msrc[f * 64 + lane];
+            f32x4 es[4];
+            const float* gsrc = ws.gates + chh * kGateFloats;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) es[mt] = *reinterpret_cast<const f32x4*>(gsrc + mt * 16 + 4 * lg);
+
+            if (!wait_ge(&sm.ready, c + 1)) break;
+            asm volatile("" ::: "memory");
+            const int slot = c % kHand;
+            half8 hsb[4], hvb[2];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) hsb[kb] = sm.hs[slot][kb][lane];
+            hvb[0] = sm.hv[slot][0][lane];
+            hvb[1] = sm.hv[slot][1][lane];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) lds_store_relaxed(&sm.cons[slot], c + 1);
+
+            uint16_t* ob = o + ((size_t)(tok0 + c * kChunk) * HV + hv) * kDV + sl * kBV + lm;
+            f32x4 qs[4], mv[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const bool okr = mt * 16 + lm < rows;
+                const uint2 z2 = {0u, 0u};
+                qs[mt] = zero4();
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const half8 qh = bf16_frag_to_half8(okr ? qr[mt][kb][0] : z2, okr ? qr[mt][kb][1] : z2);
+                    qs[mt] = mfma16(qh, hsb[kb], qs[mt]);
+                }
+                mv[mt] = mfma16(mf[mt * 2 + 0], hvb[0], zero4());
+                mv[mt] = mfma16(mf[mt * 2 + 1], hvb[1], mv[mt]);
+            }
+            if (rows == kChunk) {   // full chunk: no per-row branches
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        ob[(size_t)(mt * 16 + 4 * lg + i) * HV * kDV] =
+                            f32_to_bf16_bits(es[mt][i] * qs[mt][i] + mv[mt][i]);
+                }
+            } else {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = mt * 16 + 4 * lg + i;
+                        if (r < rows) ob[(size_t)r * HV * kDV] = f32_to_bf16_bits(es[mt][i] * qs[mt][i] + mv[mt][i]);
+                    }
+                }
+            }
         }
     }
 }
@@ -713,31 +960,34 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     Workspace ws;
     ws.Wf = reinterpret_cast<_Float16*>(base + L.wf);
     ws.Kf = reinterpret_cast<_Float16*>(base + L.kf);
-    ws.Qf = reinterpret_cast<_Float16*>(base + L.qf);
+    ws.Uf = reinterpret_cast<_Float16*>(base + L.uf);
     ws.Mf = reinterpret_cast<_Float16*>(base + L.mf);
-    ws.Uf = reinterpret_cast<float*>(base + L.uf);
-    ws.decay = reinterpret_cast<float*>(base + L.decay);
+    ws.gates = reinterpret_cast<float*>(base + L.gates);
     ws.dbgT = dump_debug ? reinterpret_cast<float*>(base + L.dbgT) : nullptr;
     ws.dbgA = dump_debug ? reinterpret_cast<float*>(base + L.dbgA) : nullptr;
     ws.dbgC = dump_debug ? reinterpret_cast<float*>(base + L.dbgC) : nullptr;
     const float scale = 1.0f / sqrtf((float)kDK);
 
     // ev (optional): kPrefillKernels + 1 events recorded around the launches
-    if (ev) hipEventRecord(ev[0], stream);
+    if (ev) (void)hipEventRecord(ev[0], stream);
     if (nch_bound > 0 && total_tokens > 0) {
-        hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nch_bound, HV), dim3(kPrepThreads), 0,
-                           stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                           static_cast<const uint16_t*>(v), g, beta, cu, N, T, HV, HK, scale, ws);
+        const int rep = HV / HK;
+        const size_t groups = (nch_bound * (size_t)HK + 7) / 8;
+        hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)(groups * 8 * rep)), dim3(kPrepThreads),
+                           0, stream, static_cast<const uint16_t*>(q),
+                           static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), g,
+                           beta, cu, N, T, HV, HK, (int)nch_bound, scale, ws);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
-    if (ev) hipEventRecord(ev[1], stream);
+    if (ev) (void)hipEventRecord(ev[1], stream);
     const int pairs = N * HV;
     const int groups = (pairs + 7) / 8;
     hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 64)), dim3(kScanThreads), 0, stream,
-                       ws, static_cast<uint16_t*>(o), s0, sf, cu, N, T, HV);
+                       ws, static_cast<const uint16_t*>(q), static_cast<uint16_t*>(o), s0, sf, cu,
+                       N, T, HV, HK);
     hipError_t err = hipGetLastError();
-    if (ev) hipEventRecord(ev[2], stream);
+    if (ev) (void)hipEventRecord(ev[2], stream);
     return err;
 }
 
