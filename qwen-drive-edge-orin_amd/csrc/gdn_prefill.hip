@@ -41,16 +41,17 @@ namespace gdn {
 namespace {
 
 constexpr int kPrepThreads = 256;
-// scan work-group: wave 0 runs the chain, waves 4-6 load its operands,
-// waves 1-3 and 7 form outputs
+// scan work-group: waves 0 and 1 run two chains, waves 4-6 load their
+// operands, waves 2, 3 and 7 form outputs
 constexpr int kScanThreads = 512;
-constexpr int kOutWaves = 4;
+constexpr int kOutWaves = 3;
 
 // Per chunk-head record sizes (elements)
 constexpr int kWfElems = kChunk * kDK;     // fp16: W, 16 A-fragments (4 row tiles x 4 k-blocks)
 constexpr int kKfElems = kDK * kChunk;     // fp16: decayed K^T, 16 A-fragments (8 dk tiles x 2 k-blocks)
 constexpr int kUfElems = kChunk * kDV;     // fp16: U in accumulator order, 8 slices x 2 tile pairs
 constexpr int kMfElems = kChunk * kChunk;  // fp16: M, 8 A-fragments (4 row tiles x 2 k-blocks)
+constexpr int kQfElems = kChunk * kDK;     // fp16: s e^c Q, 16 A-fragments (4 row tiles x 4 k-blocks)
 constexpr int kGateFloats = 128;           // fp32: s e^c [64] | e^{c_63} | unused
 constexpr int kGateDecay = 64;
 
@@ -59,6 +60,7 @@ struct Workspace {
     _Float16* Kf;
     _Float16* Uf;
     _Float16* Mf;
+    _Float16* Qf;
     float* gates;
     float* dbgT;   // optional: T = (I-A)^-1, [chunk-head][64][64]
     float* dbgA;   // optional: A, same layout
@@ -70,13 +72,14 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 // Byte layout of the workspace for `nch` chunk-heads.  The three debug
 // regions stay last: the torch binding finds them from the end.
 struct WsLayout {
-    size_t wf, kf, uf, mf, gates, dbgT, dbgA, dbgC, total;
+    size_t wf, kf, uf, mf, qf, gates, dbgT, dbgA, dbgC, total;
     __host__ explicit WsLayout(size_t nch) {
         size_t off = 0;
         wf = off;    off += align256(nch * kWfElems * 2);
         kf = off;    off += align256(nch * kKfElems * 2);
         uf = off;    off += align256(nch * kUfElems * 2);
         mf = off;    off += align256(nch * kMfElems * 2);
+        qf = off;    off += align256(nch * kQfElems * 2);
         gates = off; off += align256(nch * kGateFloats * 4);
         dbgT = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgA = off;  off += align256(nch * kChunk * kChunk * 4);
@@ -422,6 +425,18 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         half8* mdst = reinterpret_cast<half8*>(ws.Mf + ch * kMfElems);
         mdst[(wave * 2 + 0) * 64 + lane] = cat8(mh[0], mh[1]);
         mdst[(wave * 2 + 1) * 64 + lane] = cat8(mh[2], mh[3]);
+        // Q~ fragments: s e^{c_r} q_r for this wave's query rows, fp16
+        const float es = scale * exp2f(ccol);
+        half8* qdst = reinterpret_cast<half8*>(ws.Qf + ch * kQfElems);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const half8 qh = bf16_frag_to_half8(wave * 16 + lm < rows ? qr[kb][0] : z2,
+                                                wave * 16 + lm < rows ? qr[kb][1] : z2);
+            half8 o8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o8[e] = (_Float16)((float)qh[e] * es);
+            qdst[(wave * 4 + kb) * 64 + lane] = o8;
+        }
     }
     // ---- K^T fragments (dk tiles 2w, 2w+1; k-map over tokens), gathered
     // from the K rows in LDS: kt (unscaled) for W^T below, and the decayed
@@ -582,46 +597,50 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (8 waves) per (state slice, v-head, sequence)
+// scan kernel: one work-group (8 waves) per (pair of state slices, v-head,
+// sequence).  The 128 value columns of a head's state form 8 slices of 16;
+// columns evolve independently, so each slice has its own serial chain.  A
+// work-group runs two slices side by side so that they share one copy of the
+// chunk operands (W, K~^T, M, q) in LDS.
 //
-//   wave 0      the chain: keeps its 128x16 fp32 state slice in registers and
-//               per chunk forms V_n = U - W S and S <- e^{c_63} S + K~^T V_n,
-//               reading W, K~^T, U and the decay from a 3-stage LDS ring.
-//               It also warms L2 kWarmAhead chunks ahead: two strided
-//               LDS-direct loads per chunk touch this slice's eighth of the
-//               lines of W, K~^T, M and q and all of its U, so the eight
-//               slices of a head cover each line once and the loaders and
-//               output waves find their data in L2.
-//   waves 4-6   loaders: each moves a third of a chunk's chain operands
-//               (fragment-ordered, 16 bytes per lane per fragment) from
-//               L2 / HBM into the ring up to two chunks ahead of the chain.
-//   waves 1-3, 7   four output waves; the j-th forms O for chunks c = j mod 4
-//               from S_c and V_n handed over in LDS slot j.
+//   waves 0, 1  the chains of slices 2p and 2p+1: each keeps its 128x16 fp32
+//               state in registers and per chunk forms V_n = U - W S and
+//               S <- e^{c_63} S + K~^T V_n from a 3-stage LDS ring.  Wave 0
+//               also warms L2 kWarmAhead chunks ahead with strided
+//               LDS-direct loads (this work-group's quarter of the lines).
+//   waves 4-6   loaders: each moves a third of a chunk's operands (fragment
+//               ordered, 16 bytes per lane per fragment) into the ring.
+//   waves 2, 3, 7   output waves; the j-th forms O (32 columns) for chunks
+//               c = j mod 3 from S_c and V_n handed over in LDS slot j, and
+//               writes it through a private LDS tile with 16-byte stores.
+//               Each issues its next chunk's loads before its stores, so it
+//               never waits for its own stores to complete.
 // Waves meet only through LDS counters with bounded waits, never through a
-// work-group barrier, so no wave waits on a slower one it does not need.
+// work-group barrier, so no wave waits on one it does not depend on.
 // ---------------------------------------------------------------------------
+constexpr int kPairs = 4;              // work-groups (slice pairs) per (sequence, head)
 constexpr int kRing = 3;               // operand stages
-constexpr int kHand = 4;               // hand-off slots: chunk c uses slot c % kHand
+constexpr int kHand = kOutWaves;       // hand-off slots: chunk c uses slot c % kHand (= its output wave)
 constexpr int kLoaders = 3;
-constexpr int kWarmAhead = 8;          // chunks between the chain and the L2 warm-up
+constexpr int kWarmAhead = 6;          // chunks between the chains and the L2 warm-up
 constexpr int kSpinLimit = 1 << 20;    // bounded waits: ~0.1 s, then the wave gives up
-static_assert(kOutWaves == kHand, "output wave j owns hand-off slot j");
 
-// The 34 fragments of one chain step (16 of W, 16 of K~^T, 2 of U), split
-// over the loaders: fragment f lives at LDS fragment index f of a stage.
-constexpr int kStageFrags = 34;
-constexpr int kLoaderFrags[kLoaders + 1] = {0, 12, 24, 34};
+// The 36 fragments of one chunk (W 0..15, K~^T 16..31, U of the two slices
+// 32..35), split over the loaders; fragment f sits at index f of a stage.
+constexpr int kStageFrags = 36;
+constexpr int kLoaderFrags[kLoaders + 1] = {0, 12, 24, 36};
 
 struct ScanSmem {
-    half8 stage[kRing][kStageFrags][64];   // [stage][W 0..15 | K~^T 16..31 | U 32..33][lane]
-    float gd[kRing];                        // e^{c_63} of the chunk in each stage
-    half8 hs[kHand][4][64];                 // S at the start of a chunk, B-fragments
-    half8 hv[kHand][2][64];                 // V_n, B-fragments
-    uint32_t warm[256];                     // landing area of the L2 warm-up loads (never read)
-    int filled[kLoaders];                   // per loader: chunks whose part sits in the ring
-    int freed;                              // chunks whose stage the chain has finished reading
-    int ready;                              // chunks whose S / V_n sit in the hand-off slots
-    int cons[kHand];                        // per slot: 1 + the chunk an output wave last read from it
+    half8 stage[kRing][kStageFrags][64];
+    float gd[kRing];                       // e^{c_63} of the chunk in each stage
+    half8 hs[kHand][2][4][64];             // S at the start of a chunk, per chain, B-fragments
+    half8 hv[kHand][2][2][64];             // V_n, per chain, B-fragments
+    uint16_t ot[kOutWaves][kChunk][2 * kBV];   // output tiles (bf16), one per output wave
+    uint32_t warm[256];                    // landing area of the L2 warm-up loads (never read)
+    int filled[4];                         // per loader: chunks whose part sits in the ring
+    int freed[2];                          // per chain: chunks whose stage it has finished reading
+    int ready[2];                          // per chain: chunks whose hand-off part is written
+    int cons[kHand];                       // per slot: 1 + the chunk an output wave last read from it
     int red[kScanThreads / 64];
 };
 
@@ -694,6 +713,78 @@ __device__ inline bool wait_ge(const int* flag, int target) {
     return false;
 }
 
+// Wait (bounded) until every loader's counter is >= target; the three LDS
+// reads of a poll are issued together.
+__device__ inline bool wait_filled(const int* filled, int target) {
+    static_assert(kLoaders == 3, "three loader counters");
+    for (int it = 0; it < kSpinLimit; ++it) {
+        const int f0 = lds_load_relaxed(filled), f1 = lds_load_relaxed(filled + 1),
+                  f2 = lds_load_relaxed(filled + 2);
+        if (min(f0, min(f1, f2)) >= target) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+__device__ inline bool wait_both(const int* flags, int target) {
+    for (int it = 0; it < kSpinLimit; ++it) {
+        const int a = lds_load_relaxed(flags), b = lds_load_relaxed(flags + 1);
+        if (min(a, b) >= target) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// One loader wave (see the scan kernel): fragments kLoaderFrags[J] ..
+// kLoaderFrags[J+1] of every chunk, with compile-time fragment indices so
+// the loads and LDS writes are straight-line code; loader 2 also moves the
+// decay.  Two chunks are in flight: chunk c+1's loads are issued before
+// chunk c is written.  Loads past the last chunk re-read it (always in
+// bounds) and are dropped.
+template <int J>
+__device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nch, int hv, int HV,
+                           int sp, int lane) {
+    constexpr int f0 = kLoaderFrags[J], nf = kLoaderFrags[J + 1] - kLoaderFrags[J];
+    auto load = [&](int c, u32x4 (&fr)[nf], float& dg) {
+        const size_t chh = (size_t)(chunk0 + min(c, nch - 1)) * HV + hv;
+        const u32x4* wsrc = reinterpret_cast<const u32x4*>(ws.Wf + chh * kWfElems) + lane;
+        const u32x4* ksrc = reinterpret_cast<const u32x4*>(ws.Kf + chh * kKfElems) + lane;
+        const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sp * 4 * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < nf; ++i) {
+            const int f = f0 + i;
+            fr[i] = f < 16 ? wsrc[f * 64] : (f < 32 ? ksrc[(f - 16) * 64] : usrc[(f - 32) * 64]);
+        }
+        if (J == kLoaders - 1) dg = ws.gates[chh * kGateFloats + kGateDecay];
+    };
+    auto store = [&](int c, int st, const u32x4 (&fr)[nf], float dg) -> bool {
+        if (c >= kRing && !wait_both(sm.freed, c - kRing + 1)) return false;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < nf; ++i) *reinterpret_cast<u32x4*>(&sm.stage[st][f0 + i][lane]) = fr[i];
+        if (J == kLoaders - 1 && lane == 0) sm.gd[st] = dg;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) lds_store_relaxed(&sm.filled[J], c + 1);
+        return true;
+    };
+    if (nch > 0) {
+        u32x4 fa[nf], fb[nf];
+        float da = 0.f, db = 0.f;
+        load(0, fa, da);
+        int st = 0;
+        for (int c = 0; c < nch; c += 2) {
+            load(c + 1, fb, db);
+            if (!store(c, st, fa, da)) break;
+            st = (st == kRing - 1) ? 0 : st + 1;
+            if (c + 1 >= nch) break;
+            load(c + 2, fa, da);
+            if (!store(c + 1, st, fb, db)) break;
+            st = (st == kRing - 1) ? 0 : st + 1;
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     Workspace ws, const uint16_t* __restrict__ q, uint16_t* __restrict__ o,
     const float* __restrict__ s0, float* __restrict__ sf, const int32_t* __restrict__ cu, int N,
@@ -703,11 +794,12 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
 
-    // XCD-aware id: the 8 slices of one (seq, head) pair share id % 8
+    // XCD-aware id: the kPairs work-groups of one (seq, head) pair share id % 8
+    // (work-group i runs on XCD i % 8), so they read the head's operands from one L2
     const int id = blockIdx.x;
     const int xcd = id & 7, qd = id >> 3;
-    const int sl = qd & 7;
-    const int pair = (qd >> 3) * 8 + xcd;
+    const int sp = qd & (kPairs - 1);
+    const int pair = (qd / kPairs) * 8 + xcd;
     if (pair >= N * HV) return;
     const int seq = pair / HV, hv = pair - seq * HV;
     const int hk = hv / (HV / HK);
@@ -716,16 +808,18 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     const int tok0 = seq_start(cu, T, seq);
     const int nch = (len + kChunk - 1) / kChunk;
     const int chunk0 = __builtin_amdgcn_readfirstlane(chunks_before<kScanThreads>(cu, T, seq, sm.red));
-    if (tid < kLoaders) lds_store_relaxed(&sm.filled[tid], 0);
-    if (tid == 0) {
-        lds_store_relaxed(&sm.freed, 0);
-        lds_store_relaxed(&sm.ready, 0);
+    if (tid < 4) lds_store_relaxed(&sm.filled[tid], 0);
+    if (tid < 2) {
+        lds_store_relaxed(&sm.freed[tid], 0);
+        lds_store_relaxed(&sm.ready[tid], 0);
     }
     if (tid < kHand) lds_store_relaxed(&sm.cons[tid], 0);
     __syncthreads();
 
-    if (wave == 0) {
-        // ---------------- chain wave
+    if (wave < 2) {
+        // ---------------- chain waves: slice 2 sp + h
+        const int h = wave;
+        const int sl = 2 * sp + h;
         const size_t sbase = ((size_t)seq * HV + hv) * kDK * kDV + sl * kBV + lm;
         f32x4 S[8];
         if (s0) {   // one uniform branch: all 32 loads in flight together
@@ -742,45 +836,54 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
 
-        // L2 warm-up of chunk c: lane l touches one 128-byte line per load.
-        // First load: lanes 0-15 this slice's 2 KB of W, 16-31 of K~^T,
-        // 32-47 its U, 48-63 its 1 KB of M (twice).  Second load: q rows
-        // 8 sl .. 8 sl + 7 of the chunk (clamped to the sequence), 2 lines each.
+        // L2 warm-up of chunk c (wave 0 only): lane l touches one 128-byte
+        // line per load.  Load 1: lanes 0-31 this work-group's quarter of W,
+        // 32-63 of K~^T.  Load 2: lanes 0-31 the pair's U, 32-47 its quarter
+        // of M (48-63 repeat it).  Load 3: its quarter of the chunk's q rows,
+        // two lines each (clamped to the sequence; lanes 32-63 repeat).
         const uint32_t lds_warm = __builtin_amdgcn_readfirstlane(lds_u32(&sm.warm[0]));
-        const int part = lane >> 4, li = lane & 15;
         auto warm = [&](int c) {
             const size_t chh = (size_t)(chunk0 + c) * HV + hv;
-            const char* a;
-            if (part == 0) a = reinterpret_cast<const char*>(ws.Wf + chh * kWfElems) + sl * 2048 + li * 128;
-            else if (part == 1) a = reinterpret_cast<const char*>(ws.Kf + chh * kKfElems) + sl * 2048 + li * 128;
-            else if (part == 2) a = reinterpret_cast<const char*>(ws.Uf + chh * kUfElems) + sl * 2048 + li * 128;
-            else a = reinterpret_cast<const char*>(ws.Mf + chh * kMfElems) + sl * 1024 + (li & 7) * 128;
-            const int r = min(c * kChunk + 8 * sl + ((lane >> 1) & 7), len - 1);
-            const char* b = reinterpret_cast<const char*>(q + ((size_t)(tok0 + r) * HK + hk) * kDK) + (lane & 1) * 128;
+            const int l32 = lane & 31;
+            const char* a = lane < 32
+                ? reinterpret_cast<const char*>(ws.Wf + chh * kWfElems) + (sp * 32 + l32) * 128
+                : reinterpret_cast<const char*>(ws.Kf + chh * kKfElems) + (sp * 32 + l32) * 128;
+            const char* b = lane < 32
+                ? reinterpret_cast<const char*>(ws.Uf + chh * kUfElems) + sp * 4096 + l32 * 128
+                : reinterpret_cast<const char*>(ws.Mf + chh * kMfElems) + (sp * 16 + (lane & 15)) * 128;
+            const int r = min(c * kChunk + 16 * sp + (l32 >> 1), len - 1);
+            const char* qa = reinterpret_cast<const char*>(q + ((size_t)(tok0 + r) * HK + hk) * kDK) + (lane & 1) * 128;
             asm volatile(
-                "s_mov_b32 m0, %2\n\t"
+                "s_mov_b32 m0, %3\n\t"
                 "s_nop 0\n\t"
                 "global_load_lds_dwordx4 %0, off\n\t"
-                "global_load_lds_dwordx4 %1, off"
+                "global_load_lds_dwordx4 %1, off\n\t"
+                "global_load_lds_dwordx4 %2, off"
                 :
-                : "v"(a), "v"(b), "s"(lds_warm)
+                : "v"(a), "v"(b), "v"(qa), "s"(lds_warm)
                 : "memory", "m0");
         };
-        for (int c = 1; c < min(nch, kWarmAhead); ++c) warm(c);
+        if (h == 0)
+            for (int c = 1; c < min(nch, kWarmAhead); ++c) warm(c);
 
         bool ok = true;
         int st = 0;      // stage of chunk c
         int hslot = 0;   // hand-off slot of chunk c
         for (int c = 0; c < nch && ok; ++c) {
-            if (c + kWarmAhead < nch) warm(c + kWarmAhead);
-#pragma unroll
-            for (int j = 0; j < kLoaders; ++j) ok = ok && wait_ge(&sm.filled[j], c + 1);
+            if (h == 0 && c + kWarmAhead < nch) warm(c + kWarmAhead);
+            ok = ok && wait_filled(sm.filled, c + 1);
             asm volatile("" ::: "memory");
             const half8(&sg)[kStageFrags][64] = sm.stage[st];
             const float d = sm.gd[st];
-            half8 wv[16];
+            half8 wv[16], kv[16];
 #pragma unroll
             for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
+#pragma unroll
+            for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
+            const half8 u0 = sg[32 + 2 * h][lane], u1 = sg[33 + 2 * h][lane];
+            // every read of this stage has landed: hand it back to the loaders
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) lds_store_relaxed(&sm.freed[h], c + 1);
             // P = W S (64 x 16), k over dk; the four row tiles are
             // independent, so they are issued round-robin
             f32x4 P[4];
@@ -791,16 +894,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4 + kb], sb[kb], P[mt]);
             }
-            // independent of P: the decayed state and the K~^T operands
+            // independent of P: the decayed state
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = S[t] * d;
-            half8 kv[16];
-#pragma unroll
-            for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
-            const half8 u0 = sg[32][lane], u1 = sg[33][lane];
-            // every read of this stage has landed: hand it back to the loaders
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) lds_store_relaxed(&sm.freed, c + 1);
             // V_n = U - P
             f32x4 vn[4];
 #pragma unroll
@@ -827,11 +923,11 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             if (c >= kHand) ok = ok && wait_ge(&sm.cons[slot], c - kHand + 1);
             asm volatile("" ::: "memory");
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) sm.hs[slot][kb][lane] = sb[kb];
-            sm.hv[slot][0][lane] = vb[0];
-            sm.hv[slot][1][lane] = vb[1];
+            for (int kb = 0; kb < 4; ++kb) sm.hs[slot][h][kb][lane] = sb[kb];
+            sm.hv[slot][h][0][lane] = vb[0];
+            sm.hv[slot][h][1][lane] = vb[1];
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) lds_store_relaxed(&sm.ready, c + 1);
+            if (lane == 0) lds_store_relaxed(&sm.ready[h], c + 1);
 
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
@@ -845,105 +941,78 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             for (int i = 0; i < 4; ++i) sf[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV] = S[t][i];
         }
     } else if (wave >= 4 && wave < 4 + kLoaders) {
-        // ---------------- loaders: chunk c into stage c % kRing once the
-        // chain has finished reading chunk c - kRing from it
         const int j = wave - 4;
-        constexpr int kMaxFrags = 12;
-        const int f0 = kLoaderFrags[j], nf = kLoaderFrags[j + 1] - kLoaderFrags[j];
-        int st = 0;
-        for (int c = 0; c < nch; ++c) {
-            const size_t chh = (size_t)(chunk0 + c) * HV + hv;
-            const u32x4* wsrc = reinterpret_cast<const u32x4*>(ws.Wf + chh * kWfElems);
-            const u32x4* ksrc = reinterpret_cast<const u32x4*>(ws.Kf + chh * kKfElems);
-            const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sl * 2 * 64;
-            u32x4 frag[kMaxFrags];
-#pragma unroll
-            for (int i = 0; i < kMaxFrags; ++i) {
-                const int f = f0 + min(i, nf - 1);
-                const u32x4* src = f < 16 ? wsrc + f * 64 : (f < 32 ? ksrc + (f - 16) * 64 : usrc + (f - 32) * 64);
-                frag[i] = src[lane];
-            }
-            const float dgt = (j == kLoaders - 1) ? ws.gates[chh * kGateFloats + kGateDecay] : 0.f;
-            if (c >= kRing && !wait_ge(&sm.freed, c - kRing + 1)) break;
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int i = 0; i < kMaxFrags; ++i)
-                if (i < nf) *reinterpret_cast<u32x4*>(&sm.stage[st][f0 + i][lane]) = frag[i];
-            if (j == kLoaders - 1 && lane == 0) sm.gd[st] = dgt;
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) lds_store_relaxed(&sm.filled[j], c + 1);
-            st = (st == kRing - 1) ? 0 : st + 1;
-        }
+        if (j == 0) run_loader<0>(sm, ws, chunk0, nch, hv, HV, sp, lane);
+        else if (j == 1) run_loader<1>(sm, ws, chunk0, nch, hv, HV, sp, lane);
+        else run_loader<2>(sm, ws, chunk0, nch, hv, HV, sp, lane);
     } else {
-        // ---------------- output waves: chunks c = ow, ow + kOutWaves, ...
-        const int ow = wave < 4 ? wave - 1 : 3;   // waves 1, 2, 3, 7
+        // ---------------- output waves (2, 3, 7): chunks c = ow, ow + kOutWaves, ...
+        const int ow = wave == 7 ? 2 : wave - 2;
+        // operands of chunk c (clamped into range, so a look-ahead past the
+        // end re-reads the last chunk): Q~ = s e^c Q and M fragments
+        half8 qf[16], mf[8];
+        auto load_ops = [&](int c) {
+            const size_t chh = (size_t)(chunk0 + min(c, nch - 1)) * HV + hv;
+            const half8* qsrc = reinterpret_cast<const half8*>(ws.Qf + chh * kQfElems) + lane;
+            const half8* msrc = reinterpret_cast<const half8*>(ws.Mf + chh * kMfElems) + lane;
+#pragma unroll
+            for (int f = 0; f < 16; ++f) qf[f] = qsrc[f * 64];
+#pragma unroll
+            for (int f = 0; f < 8; ++f) mf[f] = msrc[f * 64];
+        };
+        if (ow < nch) load_ops(ow);
+        uint16_t(&ot)[kChunk][2 * kBV] = sm.ot[ow];
         for (int c = ow; c < nch; c += kOutWaves) {
-            const size_t chh = (size_t)(chunk0 + c) * HV + hv;
             const int rows = min(kChunk, len - c * kChunk);
-            // operands of this chunk: raw q rows (k-map over dk), M, s e^c
-            uint2 qr[4][4][2];
-            const uint16_t* qb = q + ((size_t)(tok0 + c * kChunk) * HK + hk) * kDK + 4 * lg;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const uint16_t* src = qb + (size_t)min(mt * 16 + lm, rows - 1) * HK * kDK;
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    qr[mt][kb][0] = *reinterpret_cast<const uint2*>(src + kb * 32);
-                    qr[mt][kb][1] = *reinterpret_cast<const uint2*>(src + kb * 32 + 16);
-                }
-            }
-            half8 mf[8];
-            const half8* msrc = reinterpret_cast<const half8*>(ws.Mf + chh * kMfElems);
-#pragma unroll
-            for (int f = 0; f < 8; ++f) mf[f] = msrc[f * 64 + lane];
-            f32x4 es[4];
-            const float* gsrc = ws.gates + chh * kGateFloats;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) es[mt] = *reinterpret_cast<const f32x4*>(gsrc + mt * 16 + 4 * lg);
-
-            if (!wait_ge(&sm.ready, c + 1)) break;
+            if (!wait_both(sm.ready, c + 1)) break;
             asm volatile("" ::: "memory");
-            const int slot = c % kHand;
-            half8 hsb[4], hvb[2];
+            const int slot = ow;   // c % kHand
+            half8 hsb[2][4], hvb[2][2];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) hsb[kb] = sm.hs[slot][kb][lane];
-            hvb[0] = sm.hv[slot][0][lane];
-            hvb[1] = sm.hv[slot][1][lane];
+            for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) hsb[s2][kb] = sm.hs[slot][s2][kb][lane];
+                hvb[s2][0] = sm.hv[slot][s2][0][lane];
+                hvb[s2][1] = sm.hv[slot][s2][1][lane];
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (lane == 0) lds_store_relaxed(&sm.cons[slot], c + 1);
 
-            uint16_t* ob = o + ((size_t)(tok0 + c * kChunk) * HV + hv) * kDV + sl * kBV + lm;
-            f32x4 qs[4], mv[4];
+            // O = Q~ S + M V_n for both slices; each accumulator's dependent
+            // products are issued round-robin with the other row tiles
+            f32x4 ov[2][4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const bool okr = mt * 16 + lm < rows;
-                const uint2 z2 = {0u, 0u};
-                qs[mt] = zero4();
+            for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    const half8 qh = bf16_frag_to_half8(okr ? qr[mt][kb][0] : z2, okr ? qr[mt][kb][1] : z2);
-                    qs[mt] = mfma16(qh, hsb[kb], qs[mt]);
+                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(qf[mt * 4], hsb[s2][0], zero4());
+#pragma unroll
+                for (int kb = 1; kb < 4; ++kb) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(qf[mt * 4 + kb], hsb[s2][kb], ov[s2][mt]);
                 }
-                mv[mt] = mfma16(mf[mt * 2 + 0], hvb[0], zero4());
-                mv[mt] = mfma16(mf[mt * 2 + 1], hvb[1], mv[mt]);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(mf[mt * 2 + kb], hvb[s2][kb], ov[s2][mt]);
+                }
             }
-            if (rows == kChunk) {   // full chunk: no per-row branches
+            load_ops(c + kOutWaves);   // the operand registers are free again
+            // O tile (64 rows x 32 columns, bf16) through LDS, then 16-byte
+            // stores: lane l writes row l, four 8-column pieces
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        ob[(size_t)(mt * 16 + 4 * lg + i) * HV * kDV] =
-                            f32_to_bf16_bits(es[mt][i] * qs[mt][i] + mv[mt][i]);
+                    for (int i = 0; i < 4; ++i) ot[mt * 16 + 4 * lg + i][s2 * kBV + lm] = f32_to_bf16_bits(ov[s2][mt][i]);
                 }
-            } else {
+            }
+            asm volatile("" ::: "memory");   // LDS ops of one wave complete in order
+            if (lane < rows) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(&ot[lane][0]);
+                u32x4* dst = reinterpret_cast<u32x4*>(o + ((size_t)(tok0 + c * kChunk + lane) * HV + hv) * kDV + 2 * sp * kBV);
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int r = mt * 16 + 4 * lg + i;
-                        if (r < rows) ob[(size_t)r * HV * kDV] = f32_to_bf16_bits(es[mt][i] * qs[mt][i] + mv[mt][i]);
-                    }
-                }
+                for (int p4 = 0; p4 < 4; ++p4) dst[p4] = src[p4];
             }
         }
     }
@@ -962,6 +1031,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     ws.Kf = reinterpret_cast<_Float16*>(base + L.kf);
     ws.Uf = reinterpret_cast<_Float16*>(base + L.uf);
     ws.Mf = reinterpret_cast<_Float16*>(base + L.mf);
+    ws.Qf = reinterpret_cast<_Float16*>(base + L.qf);
     ws.gates = reinterpret_cast<float*>(base + L.gates);
     ws.dbgT = dump_debug ? reinterpret_cast<float*>(base + L.dbgT) : nullptr;
     ws.dbgA = dump_debug ? reinterpret_cast<float*>(base + L.dbgA) : nullptr;
@@ -983,7 +1053,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     if (ev) (void)hipEventRecord(ev[1], stream);
     const int pairs = N * HV;
     const int groups = (pairs + 7) / 8;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 64)), dim3(kScanThreads), 0, stream,
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 8 * kPairs)), dim3(kScanThreads), 0, stream,
                        ws, static_cast<const uint16_t*>(q), static_cast<uint16_t*>(o), s0, sf, cu,
                        N, T, HV, HK);
     hipError_t err = hipGetLastError();
