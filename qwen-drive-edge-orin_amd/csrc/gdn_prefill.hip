@@ -226,6 +226,27 @@ __device__ inline f32x4 t_row4(const float* AT, int rb, int cb, int r, int c0) {
     return t;
 }
 
+// KK^T and KQ^T products of wave W: A column block W (row tiles W..3) and
+// M^T column block W (row tiles 0..W), k-blocks outermost so the five
+// accumulators' products interleave instead of waiting on each other.
+template <int W>
+__device__ inline void am_products(const bf16x8 (&ka)[4][4], const bf16x8 (&qf)[4],
+                                   f32x4 (&accA)[4], f32x4 (&accM)[4]) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        accA[mt] = zero4();
+        accM[mt] = zero4();
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int mt = W; mt < 4; ++mt) accA[mt] = mfma16_bf16(ka[mt][kb], ka[W][kb], accA[mt]);
+#pragma unroll
+        for (int mt = 0; mt <= W; ++mt) accM[mt] = mfma16_bf16(ka[mt][kb], qf[kb], accM[mt]);
+    }
+}
+
+template <bool kDbg>
 __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ g,
@@ -233,7 +254,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     int HK, int nch_bound, float scale, Workspace ws) {
     __shared__ PrepSmem sm;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
 
     // Work-group id -> (chunk, k-head, member of its GQA group).  The rep
@@ -255,7 +276,14 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 
     // ---- global loads, all issued before any is consumed.  Rows past the
     // chunk's end read the last valid row (always in bounds) and are zeroed
-    // afterwards, so no load sits behind a branch.
+    // afterwards, so no load sits behind a branch.  g and beta go first: the
+    // gates need them before anything else arrives.
+    float gv = 0.f, bv = 0.f;
+    if (wave == 0) {
+        const int r = min(lane, rows - 1);
+        gv = g[(size_t)(tok0 + r) * HV + hv];
+        bv = beta[(size_t)(tok0 + r) * HV + hv];
+    }
     // Threads 0..127 copy K rows (16-byte pieces, row-major, bf16) to LDS;
     // threads 128..255 own an 8-row x 8-column block of V for the transpose.
     const bool kthr = wave < 2;   // wave-uniform
@@ -286,12 +314,6 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
             qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
         }
     }
-    float gv = 0.f, bv = 0.f;
-    if (wave == 0) {
-        const int r = min(lane, rows - 1);
-        gv = g[(size_t)(tok0 + r) * HV + hv];
-        bv = beta[(size_t)(tok0 + r) * HV + hv];
-    }
 
     // ---- gates (wave 0): c = cumsum(g); padded rows have g = beta = 0
     if (wave == 0) {
@@ -315,7 +337,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         float* gr = ws.gates + ch * kGateFloats;
         gr[lane] = scale * ec;
         if (lane == 0) gr[kGateDecay] = exp2f(clast * kLog2e);
-        if (ws.dbgC) ws.dbgC[ch * kChunk + lane] = cs;
+        if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
     }
 
     // ---- K rows -> LDS as loaded; V block -> 8x8 register transpose -> V^T (fp16)
@@ -359,7 +381,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     // already in A-fragment order for the scan).
     {
         const uint2 z2 = {0u, 0u};
-        bf16x8 ka[4][4], kw[4], qf[4];
+        bf16x8 ka[4][4], qf[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const uint16_t* src = &sm.Kr[(mt * 16 + lm) * kKS + 4 * lg];
@@ -368,13 +390,6 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
                 ka[mt][kb] = bf16_frag(*reinterpret_cast<const uint2*>(src + kb * 32),
                                        *reinterpret_cast<const uint2*>(src + kb * 32 + 16));
         }
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            kw[kb] = ka[0][kb];
-#pragma unroll
-            for (int mt = 1; mt < 4; ++mt)
-                if (mt == wave) kw[kb] = ka[mt][kb];
-        }
         {
             const bool ok = wave * 16 + lm < rows;
 #pragma unroll
@@ -382,32 +397,33 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
                 qf[kb] = bf16_frag(ok ? qr[kb][0] : z2, ok ? qr[kb][1] : z2);
         }
         f32x4 accA[4], accM[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            accA[mt] = zero4();
-            accM[mt] = zero4();
-            if (mt >= wave) {
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) accA[mt] = mfma16_bf16(ka[mt][kb], kw[kb], accA[mt]);
-            }
-            if (mt <= wave) {
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) accM[mt] = mfma16_bf16(ka[mt][kb], qf[kb], accM[mt]);
-            }
+        switch (wave) {
+            case 0: am_products<0>(ka, qf, accA, accM); break;
+            case 1: am_products<1>(ka, qf, accA, accM); break;
+            case 2: am_products<2>(ka, qf, accA, accM); break;
+            default: am_products<3>(ka, qf, accA, accM); break;
         }
         // A: element (r = 16mt + 4lg + i, col = 16w + lm); the upper part of
         // column block w is written as zero
+        // (computed for every element, then selected: no per-element
+        // branches; the discarded exponentials may overflow harmlessly)
         const int col = wave * 16 + lm;
         const float ccol = sm.cl[col];
+        f32x4 clr[4], br[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            clr[mt] = *reinterpret_cast<const f32x4*>(&sm.cl[mt * 16 + 4 * lg]);
+            br[mt] = *reinterpret_cast<const f32x4*>(&sm.b[mt * 16 + 4 * lg]);
+        }
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = mt * 16 + 4 * lg + i;
-                float a = 0.f;
-                if (r > col) a = -sm.b[r] * accA[mt][i] * exp2f(sm.cl[r] - ccol);
+                const float av = -br[mt][i] * accA[mt][i] * __builtin_amdgcn_exp2f(clr[mt][i] - ccol);
+                const float a = r > col ? av : 0.f;
                 sm.AT[r * kMS + col] = a;
-                if (ws.dbgA) ws.dbgA[ch * kChunk * kChunk + r * kChunk + col] = a;
+                if (kDbg) ws.dbgA[ch * kChunk * kChunk + r * kChunk + col] = a;
             }
         }
         // M^T tile (mt, w): element (key ck = 16mt + 4lg + i, query col)
@@ -418,7 +434,8 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int ck = mt * 16 + 4 * lg + i;
-                val[i] = (ck <= col) ? scale * accM[mt][i] * exp2f(ccol - sm.cl[ck]) : 0.f;
+                const float mv = scale * accM[mt][i] * __builtin_amdgcn_exp2f(ccol - clr[mt][i]);
+                val[i] = ck <= col ? mv : 0.f;
             }
             mh[mt] = to_half4(val);
         }
@@ -426,7 +443,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         mdst[(wave * 2 + 0) * 64 + lane] = cat8(mh[0], mh[1]);
         mdst[(wave * 2 + 1) * 64 + lane] = cat8(mh[2], mh[3]);
         // Q~ fragments: s e^{c_r} q_r for this wave's query rows, fp16
-        const float es = scale * exp2f(ccol);
+        const float es = scale * __builtin_amdgcn_exp2f(ccol);
         half8* qdst = reinterpret_cast<half8*>(ws.Qf + ch * kQfElems);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -502,30 +519,41 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     for (int d = 1; d <= 3; ++d) {
         if (wave < 4 - d) {
             const int j = wave, i = wave + d;
-            f32x4 P = zero4();
+            // one accumulator per term kk = j + u, so the terms' products
+            // interleave; summed afterwards
+            f32x4 Pu[3];
 #pragma unroll
-            for (int kk = j; kk < i; ++kk) {
+            for (int u = 0; u < d; ++u) {
+                const int kk = j + u;
                 const f32x4 a = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * i + lm) * kMS + 16 * kk + 4 * lg]);
                 f32x4 bt;
-                if (kk == j) {
+                if (u == 0) {
 #pragma unroll
                     for (int s = 0; s < 4; ++s) bt[s] = sm.AT[(16 * j + 4 * lg + s) * kMS + 16 * j + lm];
                 } else {
                     bt = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * j + lm) * kMS + 16 * kk + 4 * lg]);
                 }
+                Pu[u] = zero4();
 #pragma unroll
-                for (int s = 0; s < 4; ++s) P = mfma_f32_16x16x4(a[s], bt[s], P);
+                for (int s = 0; s < 4; ++s) Pu[u] = mfma_f32_16x16x4(a[s], bt[s], Pu[u]);
             }
-            const f32x4 t = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * i + lm) * kMS + 16 * i + 4 * lg]);
-            f32x4 R = zero4();
+            f32x4 P = Pu[0];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) R = mfma_f32_16x16x4(t[s], P[s], R);
+            for (int u = 1; u < d; ++u) P += Pu[u];
+            const f32x4 t = *reinterpret_cast<const f32x4*>(&sm.AT[(16 * i + lm) * kMS + 16 * i + 4 * lg]);
+            f32x4 R0 = zero4(), R1 = zero4();
+#pragma unroll
+            for (int s = 0; s < 4; s += 2) {
+                R0 = mfma_f32_16x16x4(t[s], P[s], R0);
+                R1 = mfma_f32_16x16x4(t[s + 1], P[s + 1], R1);
+            }
+            const f32x4 R = R0 + R1;
             // R[s] = T_ij[4lg + s][lm] -> transposed slot (j, i)
             *reinterpret_cast<f32x4*>(&sm.AT[(16 * j + lm) * kMS + 16 * i + 4 * lg]) = R;
         }
         __syncthreads();
     }
-    if (ws.dbgT) {
+    if (kDbg) {
         for (int e = tid; e < kChunk * kChunk; e += kPrepThreads) {
             const int r = e >> 6, c = e & 63;
             float t = 0.f;
@@ -1043,7 +1071,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     if (nch_bound > 0 && total_tokens > 0) {
         const int rep = HV / HK;
         const size_t groups = (nch_bound * (size_t)HK + 7) / 8;
-        hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)(groups * 8 * rep)), dim3(kPrepThreads),
+        hipLaunchKernelGGL(dump_debug ? gdn_prep_kernel<true> : gdn_prep_kernel<false>, dim3((unsigned)(groups * 8 * rep)), dim3(kPrepThreads),
                            0, stream, static_cast<const uint16_t*>(q),
                            static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), g,
                            beta, cu, N, T, HV, HK, (int)nch_bound, scale, ws);
