@@ -47,7 +47,7 @@ constexpr int kScanThreads = 512;
 constexpr int kOutWaves = 3;
 
 // Per chunk-head record sizes (elements)
-constexpr int kWfElems = kChunk * kDK;     // fp16: W, 16 A-fragments (4 row tiles x 4 k-blocks)
+constexpr int kWfElems = kChunk * kDK;     // fp16: -W, 16 A-fragments (4 row tiles x 4 k-blocks)
 constexpr int kKfElems = kDK * kChunk;     // fp16: decayed K^T, 16 A-fragments (8 dk tiles x 2 k-blocks)
 constexpr int kUfElems = kChunk * kDV;     // fp16: U in accumulator order, 8 slices x 2 tile pairs
 constexpr int kMfElems = kChunk * kChunk;  // fp16: M, 8 A-fragments (4 row tiles x 2 k-blocks)
@@ -609,6 +609,8 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     }
     // ---- W^T = K^T (T diag(beta e^c))^T: dk tiles 2w, 2w+1 x token tiles nt.
     // The D layout of W^T tiles (2w, 2w+1) is W's A fragment (nt, k-block w).
+    // Stored negated, so the scan's product -W S accumulates onto U and
+    // yields V_n = U - W S directly.
     {
         half8* wdst = reinterpret_cast<half8*>(ws.Wf + ch * kWfElems);
 #pragma unroll
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
                 acc0 = mfma16(kt[0][1], xb[nt][1], acc0);
                 acc1 = mfma16(kt[1][1], xb[nt][1], acc1);
             }
-            wdst[(nt * 4 + wave) * 64 + lane] = cat8(to_half4(acc0), to_half4(acc1));
+            wdst[(nt * 4 + wave) * 64 + lane] = cat8(to_half4(-acc0), to_half4(-acc1));
         }
     }
 }
@@ -633,9 +635,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 //
 //   waves 0, 1  the chains of slices 2p and 2p+1: each keeps its 128x16 fp32
 //               state in registers and per chunk forms V_n = U - W S and
-//               S <- e^{c_63} S + K~^T V_n from a 3-stage LDS ring.  Wave 0
-//               also warms L2 kWarmAhead chunks ahead with strided
-//               LDS-direct loads (this work-group's quarter of the lines).
+//               S <- e^{c_63} S + K~^T V_n from a 3-stage LDS ring.
 //   waves 4-6   loaders: each moves a third of a chunk's operands (fragment
 //               ordered, 16 bytes per lane per fragment) into the ring.
 //   waves 2, 3, 7   output waves; the j-th forms O (32 columns) for chunks
@@ -650,7 +650,6 @@ constexpr int kPairs = 4;              // work-groups (slice pairs) per (sequenc
 constexpr int kRing = 3;               // operand stages
 constexpr int kHand = kOutWaves;       // hand-off slots: chunk c uses slot c % kHand (= its output wave)
 constexpr int kLoaders = 3;
-constexpr int kWarmAhead = 6;          // chunks between the chains and the L2 warm-up
 constexpr int kSpinLimit = 1 << 20;    // bounded waits: ~0.1 s, then the wave gives up
 
 // The 36 fragments of one chunk (W 0..15, K~^T 16..31, U of the two slices
@@ -664,7 +663,6 @@ struct ScanSmem {
     half8 hs[kHand][2][4][64];             // S at the start of a chunk, per chain, B-fragments
     half8 hv[kHand][2][2][64];             // V_n, per chain, B-fragments
     uint16_t ot[kOutWaves][kChunk][2 * kBV];   // output tiles (bf16), one per output wave
-    uint32_t warm[256];                    // landing area of the L2 warm-up loads (never read)
     int filled[4];                         // per loader: chunks whose part sits in the ring
     int freed[2];                          // per chain: chunks whose stage it has finished reading
     int ready[2];                          // per chain: chunks whose hand-off part is written
@@ -672,64 +670,22 @@ struct ScanSmem {
     int red[kScanThreads / 64];
 };
 
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// LDS-direct loads, issued from assembly so the compiler's wait-count pass
-// does not see them; the caller waits with vmcnt explicitly.  With M0 = LDS
-// byte address `lds` and global address `sbase + voff`, lane l's 16 bytes of
-// the transfer with immediate offset X come from sbase + voff_l + X and land
-// at lds + X + 16 * l (the offset applies to both sides).  voff_l = 16 * l
-// makes each transfer one contiguous 1 KB fragment.
-__device__ __forceinline__ void dma16x4(uint32_t voff, const void* sbase, uint32_t lds) {
-    asm volatile(
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %1\n\t"
-        "global_load_lds_dwordx4 %0, %1 offset:1024\n\t"
-        "global_load_lds_dwordx4 %0, %1 offset:2048\n\t"
-        "global_load_lds_dwordx4 %0, %1 offset:3072"
-        :
-        : "v"(voff), "s"(sbase), "s"(lds)
-        : "memory", "m0");
-}
-
-__device__ __forceinline__ void dma16x2(uint32_t voff, const void* sbase, uint32_t lds) {
-    asm volatile(
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %1\n\t"
-        "global_load_lds_dwordx4 %0, %1 offset:1024"
-        :
-        : "v"(voff), "s"(sbase), "s"(lds)
-        : "memory", "m0");
-}
-
-// 4 bytes per lane: lane l's word from sbase + voff_l lands at lds + 4 * l.
-__device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t lds) {
-    asm volatile(
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dword %0, %1"
-        :
-        : "v"(voff), "s"(sbase), "s"(lds)
-        : "memory", "m0");
-}
-
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
-    const uint64_t a = (uint64_t)(uintptr_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 __device__ __forceinline__ void lds_store_relaxed(int* p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wait until every LDS operation of this wave has completed.  The builtin
+// (rather than inline asm) lets the compiler's own wait-count tracking see
+// that the wave's LDS loads have landed, so it adds no second wait later;
+// the empty asm statements keep memory operations on their side of it.
+__device__ inline void lds_wait_all() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt 63, expcnt 7: no wait
+    asm volatile("" ::: "memory");
 }
 
 // Wait (bounded) until *flag >= target; false when the bound ran out.
@@ -741,14 +697,16 @@ __device__ inline bool wait_ge(const int* flag, int target) {
     return false;
 }
 
-// Wait (bounded) until every loader's counter is >= target; the three LDS
-// reads of a poll are issued together.
-__device__ inline bool wait_filled(const int* filled, int target) {
+// Wait (bounded) until every loader has put chunk c in the ring and the
+// hand-off slot of chunk c is free (the output wave read chunk c - kHand);
+// the four LDS reads of a poll are issued together.
+__device__ inline bool wait_chain(const ScanSmem& sm, int c, int slot) {
     static_assert(kLoaders == 3, "three loader counters");
+    const int cons_need = c >= kHand ? c - kHand + 1 : 0;
     for (int it = 0; it < kSpinLimit; ++it) {
-        const int f0 = lds_load_relaxed(filled), f1 = lds_load_relaxed(filled + 1),
-                  f2 = lds_load_relaxed(filled + 2);
-        if (min(f0, min(f1, f2)) >= target) return true;
+        const int f0 = lds_load_relaxed(&sm.filled[0]), f1 = lds_load_relaxed(&sm.filled[1]),
+                  f2 = lds_load_relaxed(&sm.filled[2]), cn = lds_load_relaxed(&sm.cons[slot]);
+        if (min(f0, min(f1, f2)) >= c + 1 && cn >= cons_need) return true;
         __builtin_amdgcn_s_sleep(1);
     }
     return false;
@@ -791,7 +749,7 @@ __device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nc
 #pragma unroll
         for (int i = 0; i < nf; ++i) *reinterpret_cast<u32x4*>(&sm.stage[st][f0 + i][lane]) = fr[i];
         if (J == kLoaders - 1 && lane == 0) sm.gd[st] = dg;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_wait_all();
         if (lane == 0) lds_store_relaxed(&sm.filled[J], c + 1);
         return true;
     };
@@ -864,105 +822,67 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
 
-        // L2 warm-up of chunk c (wave 0 only): lane l touches one 128-byte
-        // line per load.  Load 1: lanes 0-31 this work-group's quarter of W,
-        // 32-63 of K~^T.  Load 2: lanes 0-31 the pair's U, 32-47 its quarter
-        // of M (48-63 repeat it).  Load 3: its quarter of the chunk's q rows,
-        // two lines each (clamped to the sequence; lanes 32-63 repeat).
-        const uint32_t lds_warm = __builtin_amdgcn_readfirstlane(lds_u32(&sm.warm[0]));
-        auto warm = [&](int c) {
-            const size_t chh = (size_t)(chunk0 + c) * HV + hv;
-            const int l32 = lane & 31;
-            const char* a = lane < 32
-                ? reinterpret_cast<const char*>(ws.Wf + chh * kWfElems) + (sp * 32 + l32) * 128
-                : reinterpret_cast<const char*>(ws.Kf + chh * kKfElems) + (sp * 32 + l32) * 128;
-            const char* b = lane < 32
-                ? reinterpret_cast<const char*>(ws.Uf + chh * kUfElems) + sp * 4096 + l32 * 128
-                : reinterpret_cast<const char*>(ws.Mf + chh * kMfElems) + (sp * 16 + (lane & 15)) * 128;
-            const int r = min(c * kChunk + 16 * sp + (l32 >> 1), len - 1);
-            const char* qa = reinterpret_cast<const char*>(q + ((size_t)(tok0 + r) * HK + hk) * kDK) + (lane & 1) * 128;
-            asm volatile(
-                "s_mov_b32 m0, %3\n\t"
-                "s_nop 0\n\t"
-                "global_load_lds_dwordx4 %0, off\n\t"
-                "global_load_lds_dwordx4 %1, off\n\t"
-                "global_load_lds_dwordx4 %2, off"
-                :
-                : "v"(a), "v"(b), "v"(qa), "s"(lds_warm)
-                : "memory", "m0");
-        };
-        if (h == 0)
-            for (int c = 1; c < min(nch, kWarmAhead); ++c) warm(c);
-
         bool ok = true;
         int st = 0;      // stage of chunk c
         int hslot = 0;   // hand-off slot of chunk c
         for (int c = 0; c < nch && ok; ++c) {
-            if (h == 0 && c + kWarmAhead < nch) warm(c + kWarmAhead);
-            ok = ok && wait_filled(sm.filled, c + 1);
+            // chunk c's operands are in the ring and its hand-off slot is
+            // free (its previous chunk, c - kHand, was read): one poll
+            ok = ok && wait_chain(sm, c, hslot);
             asm volatile("" ::: "memory");
+            // S_c goes to the hand-off slot now: it is known before the
+            // chunk's products
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) sm.hs[hslot][h][kb][lane] = sb[kb];
             const half8(&sg)[kStageFrags][64] = sm.stage[st];
-            const float d = sm.gd[st];
             half8 wv[16], kv[16];
 #pragma unroll
             for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
+            const half8 u0 = sg[32 + 2 * h][lane], u1 = sg[33 + 2 * h][lane];
+            const float d = sm.gd[st];
 #pragma unroll
             for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
-            const half8 u0 = sg[32 + 2 * h][lane], u1 = sg[33 + 2 * h][lane];
             // every read of this stage has landed: hand it back to the loaders
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_wait_all();
             if (lane == 0) lds_store_relaxed(&sm.freed[h], c + 1);
-            // P = W S (64 x 16), k over dk; the four row tiles are
-            // independent, so they are issued round-robin
+            // V_n = U - W S (64 x 16): the stored -W accumulates onto U; k
+            // over dk, the four row tiles independent and issued round-robin
             f32x4 P[4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4], sb[0], zero4());
+            for (int i = 0; i < 4; ++i) {
+                P[0][i] = (float)u0[i];
+                P[1][i] = (float)u0[4 + i];
+                P[2][i] = (float)u1[i];
+                P[3][i] = (float)u1[4 + i];
+            }
 #pragma unroll
-            for (int kb = 1; kb < 4; ++kb) {
+            for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4 + kb], sb[kb], P[mt]);
             }
             // independent of P: the decayed state
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = S[t] * d;
-            // V_n = U - P
-            f32x4 vn[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                vn[0][i] = (float)u0[i] - P[0][i];
-                vn[1][i] = (float)u0[4 + i] - P[1][i];
-                vn[2][i] = (float)u1[i] - P[2][i];
-                vn[3][i] = (float)u1[4 + i] - P[3][i];
-            }
             half8 vb[2];
-            vb[0] = cat8(to_half4(vn[0]), to_half4(vn[1]));
-            vb[1] = cat8(to_half4(vn[2]), to_half4(vn[3]));
+            vb[0] = cat8(to_half4(P[0]), to_half4(P[1]));
+            vb[1] = cat8(to_half4(P[2]), to_half4(P[3]));
+            sm.hv[hslot][h][0][lane] = vb[0];
+            sm.hv[hslot][h][1][lane] = vb[1];
             // S = d S + K~^T V_n (128 x 16), k over tokens; eight independent
             // tiles, issued round-robin
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 0], vb[0], S[t]);
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 1], vb[1], S[t]);
-
-            // hand S_c (its fp16 copy sb) and V_n to the output waves while
-            // the products run
-            const int slot = hslot;
-            hslot = (hslot == kHand - 1) ? 0 : hslot + 1;
-            if (c >= kHand) ok = ok && wait_ge(&sm.cons[slot], c - kHand + 1);
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) sm.hs[slot][h][kb][lane] = sb[kb];
-            sm.hv[slot][h][0][lane] = vb[0];
-            sm.hv[slot][h][1][lane] = vb[1];
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // the hand-off writes were issued before the products: publish
+            lds_wait_all();
             if (lane == 0) lds_store_relaxed(&sm.ready[h], c + 1);
+            hslot = (hslot == kHand - 1) ? 0 : hslot + 1;
 
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
             st = (st == kRing - 1) ? 0 : st + 1;
         }
-        // the warm-up loads land in LDS: drain them before the wave ends
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
@@ -1003,7 +923,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
                 hvb[s2][0] = sm.hv[slot][s2][0][lane];
                 hvb[s2][1] = sm.hv[slot][s2][1][lane];
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_wait_all();
             if (lane == 0) lds_store_relaxed(&sm.cons[slot], c + 1);
 
             // O = Q~ S + M V_n for both slices; each accumulator's dependent
