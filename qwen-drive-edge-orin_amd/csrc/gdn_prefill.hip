@@ -51,7 +51,7 @@ constexpr int kWfElems = kChunk * kDK;     // fp16: -W, 16 A-fragments (4 row ti
 constexpr int kKfElems = kDK * kChunk;     // fp16: decayed K^T, 16 A-fragments (8 dk tiles x 2 k-blocks)
 constexpr int kUfElems = kChunk * kDV;     // fp16: U in accumulator order, 8 slices x 2 tile pairs
 constexpr int kMfElems = kChunk * kChunk;  // fp16: M, 8 A-fragments (4 row tiles x 2 k-blocks)
-constexpr int kQfElems = kChunk * kDK;     // fp16: s e^c Q, 16 A-fragments (4 row tiles x 4 k-blocks)
+constexpr int kQfElems = kChunk * kDK;     // fp16: Q, 16 fragments (4 row tiles x 4 k-blocks), per GQA group
 constexpr int kGateFloats = 128;           // fp32: s e^c [64] | e^{c_63} | unused
 constexpr int kGateDecay = 64;
 
@@ -60,7 +60,7 @@ struct Workspace {
     _Float16* Kf;
     _Float16* Uf;
     _Float16* Mf;
-    _Float16* Qf;
+    _Float16* Qf;   // at the chunk-head of each GQA group's first v-head
     float* gates;
     float* dbgT;   // optional: T = (I-A)^-1, [chunk-head][64][64]
     float* dbgA;   // optional: A, same layout
@@ -199,15 +199,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 // prep kernel: one work-group (4 waves) per (chunk, v-head)
 // ---------------------------------------------------------------------------
 constexpr int kKS = kDK + 8;      // bf16 K row pitch: 136 halves (272 B, 16-byte aligned)
-constexpr int kTS = kChunk + 4;   // fp16 V^T row pitch: 68 halves
 constexpr int kMS = kChunk + 4;   // fp32 A / T row pitch: 68 floats
 
 struct PrepSmem {
     uint16_t Kr[kChunk * kKS];   // K rows (bf16, as loaded), [token][dk]
-    _Float16 Vt[kDV * kTS];      // V^T (fp16), [dv][token]; first 1 KB doubles as scan scratch
     // A (strictly lower, row-major) on entry.  The inverse overwrites it in
     // place: diagonal blocks T_ii row-major at (i, i); T_ij (i > j) stored
-    // transposed at block (j, i), where A is zero and never read.
+    // transposed at block (j, i), where A is zero and never read.  Its first
+    // 1 KB is the sequence-lookup scratch before that.
     float AT[kChunk * kMS];
     float cl[kChunk];   // c * log2(e)
     float b[kChunk];    // beta
@@ -224,6 +223,20 @@ __device__ inline f32x4 t_row4(const float* AT, int rb, int cb, int r, int c0) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) t[e] = AT[(c0 + e) * kMS + r];
     return t;
+}
+
+// Selector fragments: E_h is the 32 x 16 block of the identity that picks
+// columns 16h .. 16h+15 of a 32-wide k-block, as an MFMA B operand
+// (lane (g, l) holds rows kmap(g, j), column l).  X E_h copies a 16-column
+// tile of X exactly (one product per output) into the accumulator layout,
+// i.e. into the order in which a pair of such tiles is the k-mapped operand
+// of the transposed product.
+__device__ inline bf16x8 selector_frag(int h, int lg, int lm) {
+    bf16x8 e;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        e[j] = (lg == (lm >> 2) && j == 4 * h + (lm & 3)) ? (__bf16)1.0f : (__bf16)0.0f;
+    return e;
 }
 
 // KK^T and KQ^T products of wave W: A column block W (row tiles W..3) and
@@ -269,7 +282,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     const int hv = hk * rep + (rest % rep);
 
     int seq, tok0, rows;
-    if (!locate_chunk<kPrepThreads>(cu, N, T, cid, reinterpret_cast<int*>(sm.Vt), seq, tok0,
+    if (!locate_chunk<kPrepThreads>(cu, N, T, cid, reinterpret_cast<int*>(sm.AT), seq, tok0,
                                     rows))
         return;
     const size_t ch = (size_t)cid * HV + hv;
@@ -284,23 +297,27 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         gv = g[(size_t)(tok0 + r) * HV + hv];
         bv = beta[(size_t)(tok0 + r) * HV + hv];
     }
-    // Threads 0..127 copy K rows (16-byte pieces, row-major, bf16) to LDS;
-    // threads 128..255 own an 8-row x 8-column block of V for the transpose.
-    const bool kthr = wave < 2;   // wave-uniform
-    const int blk = tid & 127, rg = blk & 7, cc = blk >> 3;
-    u32x4 raw[8];
+    // K rows (16-byte pieces, row-major, bf16) go to LDS: thread t copies
+    // pieces t, t + 256, ... (row piece / 16, columns 8 (piece % 16) ..).
+    u32x4 raw[4];
     {
-        // K piece ii: row (blk + 128 ii) / 16, columns 8 * (blk % 16) ..;
-        // V piece ii: row 8 rg + ii, columns 8 cc ..
-        const uint16_t* base = kthr ? k + ((size_t)tok0 * HK + hk) * kDK + 8 * (blk & 15)
-                                    : v + ((size_t)tok0 * HV + hv) * kDV + 8 * cc;
-        const size_t pitch = (size_t)(kthr ? HK : HV) * kDK;
-        const int r0 = kthr ? (blk >> 4) : 8 * rg;
-        const int rstep = kthr ? 8 : 1;
+        const uint16_t* base = k + ((size_t)tok0 * HK + hk) * kDK + 8 * (tid & 15);
 #pragma unroll
-        for (int ii = 0; ii < 8; ++ii) {
-            const int r = min(r0 + rstep * ii, rows - 1);
-            raw[ii] = *reinterpret_cast<const u32x4*>(base + (size_t)r * pitch);
+        for (int ii = 0; ii < 4; ++ii) {
+            const int r = min((tid >> 4) + 16 * ii, rows - 1);
+            raw[ii] = *reinterpret_cast<const u32x4*>(base + (size_t)r * HK * kDK);
+        }
+    }
+    // this wave's V rows for value columns 32 w .. 32 w + 31 (the U slices
+    // 2w, 2w+1), k-mapped like an A operand: token tile tt, row 16 tt + lm
+    uint2 vr[4][2];
+    {
+        const uint16_t* vs = v + (size_t)hv * kDV + 32 * wave + 4 * lg;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const uint16_t* vrow = vs + (size_t)(tok0 + min(16 * tt + lm, rows - 1)) * HV * kDV;
+            vr[tt][0] = *reinterpret_cast<const uint2*>(vrow);
+            vr[tt][1] = *reinterpret_cast<const uint2*>(vrow + 16);
         }
     }
     // this wave's Q rows (k-map over dk); bf16 straight into the MFMA
@@ -340,38 +357,13 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
     }
 
-    // ---- K rows -> LDS as loaded; V block -> 8x8 register transpose -> V^T (fp16)
-    {
-        // rows past the chunk's end are zeroed (padding rows contribute nothing)
-        if (kthr) {
+    // ---- K rows -> LDS as loaded; rows past the chunk's end are zeroed
+    // (padding rows contribute nothing)
 #pragma unroll
-            for (int ii = 0; ii < 8; ++ii) {
-                const int r = (blk >> 4) + 8 * ii;
-                const uint32_t m = r < rows ? 0xffffffffu : 0u;
-                *reinterpret_cast<u32x4*>(&sm.Kr[r * kKS + 8 * (blk & 15)]) = raw[ii] & m;
-            }
-        } else {
-            half8 hrow[8];
-#pragma unroll
-            for (int ii = 0; ii < 8; ++ii) {
-                const uint32_t m = 8 * rg + ii < rows ? 0xffffffffu : 0u;
-                const u32x4 w = raw[ii] & m;
-                const uint4 w4 = {w[0], w[1], w[2], w[3]};
-                hrow[ii] = bf16x8_to_half8(w4);
-            }
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                half4 lo, hi;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    lo[e] = hrow[e][jj];
-                    hi[e] = hrow[4 + e][jj];
-                }
-                half4* dst = reinterpret_cast<half4*>(&sm.Vt[(8 * cc + jj) * kTS + 8 * rg]);
-                dst[0] = lo;
-                dst[1] = hi;
-            }
-        }
+    for (int ii = 0; ii < 4; ++ii) {
+        const int r = (tid >> 4) + 16 * ii;
+        const uint32_t m = r < rows ? 0xffffffffu : 0u;
+        *reinterpret_cast<u32x4*>(&sm.Kr[r * kKS + 8 * (tid & 15)]) = raw[ii] & m;
     }
     __syncthreads();
 
@@ -379,6 +371,9 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     // Wave w owns column block j in [16w, 16w+16) of A and query-row block
     // r in [16w, 16w+16) of M (computed as M^T = K Q^T so the accumulator is
     // already in A-fragment order for the scan).
+    bf16x8 sel[2];
+    sel[0] = selector_frag(0, lg, lm);
+    sel[1] = selector_frag(1, lg, lm);
     {
         const uint2 z2 = {0u, 0u};
         bf16x8 ka[4][4], qf[4];
@@ -442,24 +437,33 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         half8* mdst = reinterpret_cast<half8*>(ws.Mf + ch * kMfElems);
         mdst[(wave * 2 + 0) * 64 + lane] = cat8(mh[0], mh[1]);
         mdst[(wave * 2 + 1) * 64 + lane] = cat8(mh[2], mh[3]);
-        // Q~ fragments: s e^{c_r} q_r for this wave's query rows, fp16
-        const float es = scale * __builtin_amdgcn_exp2f(ccol);
-        half8* qdst = reinterpret_cast<half8*>(ws.Qf + ch * kQfElems);
+        // this wave's Q rows as fp16 fragments; the v-heads of a GQA group
+        // share them, so only the group's first writes them
+        if (hv == hk * rep) {
+            half8* qdst = reinterpret_cast<half8*>(ws.Qf + ch * kQfElems);
+            const bool ok = wave * 16 + lm < rows;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const half8 qh = bf16_frag_to_half8(wave * 16 + lm < rows ? qr[kb][0] : z2,
-                                                wave * 16 + lm < rows ? qr[kb][1] : z2);
-            half8 o8;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o8[e] = (_Float16)((float)qh[e] * es);
-            qdst[(wave * 4 + kb) * 64 + lane] = o8;
+            for (int kb = 0; kb < 4; ++kb)
+                qdst[(wave * 4 + kb) * 64 + lane] = bf16_frag_to_half8(ok ? qr[kb][0] : z2, ok ? qr[kb][1] : z2);
         }
     }
-    // ---- K^T fragments (dk tiles 2w, 2w+1; k-map over tokens), gathered
-    // from the K rows in LDS: kt (unscaled) for W^T below, and the decayed
-    // e^{c_63 - c_tau} k_tau[dk] fragments the scan streams.
+    // ---- K^T fragments (dk tiles 2w, 2w+1; k-map over tokens): the
+    // accumulator-layout K tiles of token tiles 2kb, 2kb+1 form k-block kb.
+    // kt (unscaled) feeds W^T below; the decayed e^{c_63 - c_tau} k_tau[dk]
+    // fragments are the scan's.
     half8 kt[2][2];
     {
+        // K tiles (token tile tt, dk tile 2w + p) in accumulator layout, from
+        // this wave's dk block of the K rows
+        f32x4 kd[2][4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const uint16_t* src = &sm.Kr[(tt * 16 + lm) * kKS + 32 * wave + 4 * lg];
+            const bf16x8 kw = bf16_frag(*reinterpret_cast<const uint2*>(src),
+                                        *reinterpret_cast<const uint2*>(src + 16));
+            kd[0][tt] = mfma16_bf16(kw, sel[0], zero4());
+            kd[1][tt] = mfma16_bf16(kw, sel[1], zero4());
+        }
         half8* kdst = reinterpret_cast<half8*>(ws.Kf + ch * kKfElems);
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
@@ -467,15 +471,9 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const int k0 = kb * 32 + 4 * lg;
-                const uint16_t* src = &sm.Kr[k0 * kKS + mt * 16 + lm];
                 const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.ed[k0]);
                 const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.ed[k0 + 16]);
-                f32x4 klo, khi;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    klo[j] = bf16_bits_to_f32(src[j * kKS]);
-                    khi[j] = bf16_bits_to_f32(src[(16 + j) * kKS]);
-                }
+                const f32x4 klo = kd[p][2 * kb], khi = kd[p][2 * kb + 1];
                 kt[p][kb] = cat8(to_half4(klo), to_half4(khi));
                 kdst[(mt * 2 + kb) * 64 + lane] = cat8(to_half4(klo * d0), to_half4(khi * d1));
             }
@@ -585,17 +583,21 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     // ---- U = (T diag(beta)) V: slices nt = 2w, 2w+1, all four row tiles.
     // T is lower triangular: row tiles 0 and 1 see only tokens 0..31.
     {
+        bf16x8 vrf[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) vrf[tt] = bf16_frag(vr[tt][0], vr[tt][1]);
         half8* udst = reinterpret_cast<half8*>(ws.Uf + ch * kUfElems);
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int nt = wave * 2 + p;
+            // V tiles (token tile tt, value tile nt) in accumulator layout;
+            // token tiles 2kb, 2kb+1 form the k-block kb operand
+            f32x4 vd[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) vd[tt] = mfma16_bf16(vrf[tt], sel[p], zero4());
             half8 vb[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const _Float16* src = &sm.Vt[(nt * 16 + lm) * kTS + kb * 32 + 4 * lg];
-                vb[kb] = cat8(*reinterpret_cast<const half4*>(src),
-                              *reinterpret_cast<const half4*>(src + 16));
-            }
+            for (int kb = 0; kb < 2; ++kb) vb[kb] = cat8(to_half4(vd[2 * kb]), to_half4(vd[2 * kb + 1]));
             half4 uh[4];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
@@ -897,14 +899,21 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
         // ---------------- output waves (2, 3, 7): chunks c = ow, ow + kOutWaves, ...
         const int ow = wave == 7 ? 2 : wave - 2;
         // operands of chunk c (clamped into range, so a look-ahead past the
-        // end re-reads the last chunk): Q~ = s e^c Q and M fragments
+        // end re-reads the last chunk): Q fragments (fp16, row tile mt,
+        // k-block kb, from the GQA group's first v-head), s e^c of the
+        // lane's tokens and M fragments
         half8 qf[16], mf[8];
+        float es[4];
+        const int hq = hk * (HV / HK);
         auto load_ops = [&](int c) {
-            const size_t chh = (size_t)(chunk0 + min(c, nch - 1)) * HV + hv;
-            const half8* qsrc = reinterpret_cast<const half8*>(ws.Qf + chh * kQfElems) + lane;
+            const size_t cb = (size_t)(chunk0 + min(c, nch - 1)) * HV;
+            const size_t chh = cb + hv;
+            const half8* qsrc = reinterpret_cast<const half8*>(ws.Qf + (cb + hq) * kQfElems) + lane;
             const half8* msrc = reinterpret_cast<const half8*>(ws.Mf + chh * kMfElems) + lane;
 #pragma unroll
             for (int f = 0; f < 16; ++f) qf[f] = qsrc[f * 64];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) es[mt] = ws.gates[chh * kGateFloats + 16 * mt + lm];
 #pragma unroll
             for (int f = 0; f < 8; ++f) mf[f] = msrc[f * 64];
         };
@@ -926,33 +935,41 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             lds_wait_all();
             if (lane == 0) lds_store_relaxed(&sm.cons[slot], c + 1);
 
-            // O = Q~ S + M V_n for both slices; each accumulator's dependent
-            // products are issued round-robin with the other row tiles
+            // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T for both slices (operands
+            // swapped so each lane holds four consecutive columns of one
+            // token, whose s e^c then scales them); each accumulator's
+            // dependent products are issued round-robin
             f32x4 ov[2][4];
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(qf[mt * 4], hsb[s2][0], zero4());
+                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hsb[s2][0], qf[mt * 4], zero4());
 #pragma unroll
                 for (int kb = 1; kb < 4; ++kb) {
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(qf[mt * 4 + kb], hsb[s2][kb], ov[s2][mt]);
+                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hsb[s2][kb], qf[mt * 4 + kb], ov[s2][mt]);
                 }
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = ov[s2][mt] * es[mt];
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(mf[mt * 2 + kb], hvb[s2][kb], ov[s2][mt]);
+                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hvb[s2][kb], mf[mt * 2 + kb], ov[s2][mt]);
                 }
             }
             load_ops(c + kOutWaves);   // the operand registers are free again
             // O tile (64 rows x 32 columns, bf16) through LDS, then 16-byte
-            // stores: lane l writes row l, four 8-column pieces
+            // stores: lane (g, l) holds token 16 mt + l, columns 16 s2 + 4g ..
+            // + 3 (one 8-byte write each); lane l then writes row l, four
+            // 8-column pieces
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) ot[mt * 16 + 4 * lg + i][s2 * kBV + lm] = f32_to_bf16_bits(ov[s2][mt][i]);
+                    uint2 pk;
+                    pk.x = (uint32_t)f32_to_bf16_bits(ov[s2][mt][0]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][1]) << 16);
+                    pk.y = (uint32_t)f32_to_bf16_bits(ov[s2][mt][2]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][3]) << 16);
+                    *reinterpret_cast<uint2*>(&ot[mt * 16 + lm][s2 * kBV + 4 * lg]) = pk;
                 }
             }
             asm volatile("" ::: "memory");   // LDS ops of one wave complete in order
