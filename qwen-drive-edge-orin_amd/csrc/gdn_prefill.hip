@@ -827,11 +827,21 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
         bool ok = true;
         int st = 0;      // stage of chunk c
         int hslot = 0;   // hand-off slot of chunk c
+        // counters polled during the previous chunk (monotonic, so values
+        // that already satisfy a wait let the chain skip the wait)
+        int pf0 = 0, pf1 = 0, pf2 = 0, pfc = 0;
         for (int c = 0; c < nch && ok; ++c) {
             // chunk c's operands are in the ring and its hand-off slot is
-            // free (its previous chunk, c - kHand, was read): one poll
-            ok = ok && wait_chain(sm, c, hslot);
-            asm volatile("" ::: "memory");
+            // free (its previous chunk, c - kHand, was read)
+            const int cons_need = c >= kHand ? c - kHand + 1 : 0;
+            if (min(pf0, min(pf1, pf2)) < c + 1 || pfc < cons_need) ok = ok && wait_chain(sm, c, hslot);
+            // the previous chunk's stage reads and hand-off writes have
+            // landed: publish both
+            lds_wait_all();
+            if (lane == 0 && c > 0) {
+                lds_store_relaxed(&sm.freed[h], c);
+                lds_store_relaxed(&sm.ready[h], c);
+            }
             // S_c goes to the hand-off slot now: it is known before the
             // chunk's products
 #pragma unroll
@@ -844,9 +854,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             const float d = sm.gd[st];
 #pragma unroll
             for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
-            // every read of this stage has landed: hand it back to the loaders
-            lds_wait_all();
-            if (lane == 0) lds_store_relaxed(&sm.freed[h], c + 1);
             // V_n = U - W S (64 x 16): the stored -W accumulates onto U; k
             // over dk, the four row tiles independent and issued round-robin
             f32x4 P[4];
@@ -862,6 +869,12 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4 + kb], sb[kb], P[mt]);
             }
+            // the next chunk's counters, read while the products run
+            const int hsn = (hslot == kHand - 1) ? 0 : hslot + 1;
+            pf0 = lds_load_relaxed(&sm.filled[0]);
+            pf1 = lds_load_relaxed(&sm.filled[1]);
+            pf2 = lds_load_relaxed(&sm.filled[2]);
+            pfc = lds_load_relaxed(&sm.cons[hsn]);
             // independent of P: the decayed state
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = S[t] * d;
@@ -876,14 +889,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 0], vb[0], S[t]);
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 1], vb[1], S[t]);
-            // the hand-off writes were issued before the products: publish
-            lds_wait_all();
-            if (lane == 0) lds_store_relaxed(&sm.ready[h], c + 1);
-            hslot = (hslot == kHand - 1) ? 0 : hslot + 1;
-
+            hslot = hsn;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
             st = (st == kRing - 1) ? 0 : st + 1;
+        }
+        // the last chunk's stage reads and hand-off
+        lds_wait_all();
+        if (lane == 0 && ok) {
+            lds_store_relaxed(&sm.freed[h], nch);
+            lds_store_relaxed(&sm.ready[h], nch);
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
