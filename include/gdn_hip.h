@@ -68,6 +68,20 @@ hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k, const void
                                         void* workspace, size_t workspace_bytes,
                                         hipStream_t stream, hipEvent_t* events, int n_events);
 
+/* One kernel of deltanet_chunk_prefill on its own (no counterpart in the
+ * reference; for benchmarks that time back-to-back launches of a single
+ * kernel).  kernel 0 (prep) fills the workspace from the inputs; kernel 1
+ * (scan) reads a workspace that kernel 0 filled for the same arguments and
+ * writes o and final_state.  Arguments as in deltanet_chunk_prefill
+ * (dump_debug = 0); kernel outside [0, deltanet_prefill_kernel_count())
+ * returns hipErrorInvalidValue. */
+hipError_t deltanet_chunk_prefill_kernel(const void* q, const void* k, const void* v,
+                                         const float* g, const float* beta, void* o,
+                                         const float* initial_state, float* final_state, int B,
+                                         int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                         void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream, int kernel);
+
 /* Names of the reference's bf16-wmma o-pass twin (kernels/chunk_delta_cuda_tco.h:39,47);
  * same implementation and workspace as the two entries above. */
 size_t deltanet_tcop_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int chunk_size);

@@ -1002,7 +1002,8 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
                           const float* beta, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
-                          hipStream_t stream, int dump_debug, hipEvent_t* ev = nullptr) {
+                          hipStream_t stream, int dump_debug, hipEvent_t* ev = nullptr,
+                          int only = -1) {
     const WsLayout L(nch_bound * (size_t)HV);
     if (workspace_bytes < L.total) return hipErrorInvalidValue;
     char* base = static_cast<char*>(workspace);
@@ -1020,7 +1021,8 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
 
     // ev (optional): kPrefillKernels + 1 events recorded around the launches
     if (ev) (void)hipEventRecord(ev[0], stream);
-    if (nch_bound > 0 && total_tokens > 0) {
+    // only (optional): launch just that kernel of the pipeline (0 prep, 1 scan)
+    if (nch_bound > 0 && total_tokens > 0 && only != 1) {
         const int rep = HV / HK;
         const size_t groups = (nch_bound * (size_t)HK + 7) / 8;
         hipLaunchKernelGGL(dump_debug ? gdn_prep_kernel<true> : gdn_prep_kernel<false>, dim3((unsigned)(groups * 8 * rep)), dim3(kPrepThreads),
@@ -1031,6 +1033,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
         if (err != hipSuccess) return err;
     }
     if (ev) (void)hipEventRecord(ev[1], stream);
+    if (only == 0) return hipSuccess;
     const int pairs = N * HV;
     const int groups = (pairs + 7) / 8;
     hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 8 * kPairs)), dim3(kScanThreads), 0, stream,
@@ -1098,6 +1101,22 @@ extern "C" hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k,
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
     return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
                           HV, HQK, nc, workspace, workspace_bytes, stream, 0, events);
+}
+
+extern "C" hipError_t deltanet_chunk_prefill_kernel(const void* q, const void* k, const void* v,
+                                                    const float* g, const float* beta, void* o,
+                                                    const float* initial_state,
+                                                    float* final_state, int B, int T, int HV,
+                                                    int HQK, int DK, int DV, int chunk_size,
+                                                    void* workspace, size_t workspace_bytes,
+                                                    hipStream_t stream, int kernel) {
+    if (kernel < 0 || kernel >= kPrefillKernels) return hipErrorInvalidValue;
+    if (!dims_ok(HV, HQK, DK, DV, chunk_size) || B <= 0 || T < 0) return hipErrorInvalidValue;
+    if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
+                          HV, HQK, nc, workspace, workspace_bytes, stream, 0, nullptr, kernel);
 }
 
 extern "C" size_t deltanet_prefill_varlen_workspace_size(int total_tokens, int num_seqs, int HV,

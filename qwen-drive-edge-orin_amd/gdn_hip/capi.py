@@ -39,6 +39,8 @@ _PROTOS = {
     "deltanet_prefill_kernel_name": (ct.c_char_p, [c_int]),
     "deltanet_chunk_prefill_timed": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
                                      [vp, c_size_t, hipStream_t, vp, c_int]),
+    "deltanet_chunk_prefill_kernel": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
+                                      [vp, c_size_t, hipStream_t, c_int]),
     "gdn_gated_rmsnorm_forward": (hipError_t, [vp, vp, vp, vp, c_int64, c_int, c_float, c_int,
                                                c_int, hipStream_t]),
 }

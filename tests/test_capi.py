@@ -85,6 +85,19 @@ def test_timed_prefill_rejects_bad_events(lib):
     assert lib.deltanet_chunk_prefill_timed(*args, ev, n + 1) == INVALID   # null events
 
 
+def test_single_kernel_rejects_bad_index(lib):
+    n = lib.deltanet_prefill_kernel_count()
+    a = _prefill_args()
+    args = [a[x] for x in ("q", "k", "v", "g", "beta", "o", "s0", "sf", "B", "T", "HV", "HQK",
+                           "DK", "DV", "chunk", "ws", "ws_bytes", "stream")]
+    assert lib.deltanet_chunk_prefill_kernel(*args, -1) == INVALID
+    assert lib.deltanet_chunk_prefill_kernel(*args, n) == INVALID
+    bad = _prefill_args(DK=64)
+    bargs = [bad[x] for x in ("q", "k", "v", "g", "beta", "o", "s0", "sf", "B", "T", "HV", "HQK",
+                              "DK", "DV", "chunk", "ws", "ws_bytes", "stream")]
+    assert lib.deltanet_chunk_prefill_kernel(*bargs, 0) == INVALID
+
+
 def test_varlen_rejects_on_host(lib):
     f = lib.deltanet_chunk_prefill_varlen
     ok = [1, 1, 1, 1, 1, 1, None, 1, 1, 2, 128, 4, 2, 128, 128, 64, 1, 1 << 40, None, 0]
