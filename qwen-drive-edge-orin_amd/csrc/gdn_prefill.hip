@@ -41,9 +41,9 @@ namespace gdn {
 namespace {
 
 constexpr int kPrepThreads = 256;
-// scan work-group: waves 0 and 1 run two chains, waves 4-6 load their
-// operands, waves 2, 3 and 7 form outputs
-constexpr int kScanThreads = 512;
+// scan work-group: wave 0 runs the chain of one state slice, waves 1-3 load
+// its operands, waves 4-6 form outputs
+constexpr int kScanThreads = 448;
 constexpr int kOutWaves = 3;
 
 // Per chunk-head record sizes (elements)
@@ -629,18 +629,18 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (8 waves) per (pair of state slices, v-head,
-// sequence).  The 128 value columns of a head's state form 8 slices of 16;
-// columns evolve independently, so each slice has its own serial chain.  A
-// work-group runs two slices side by side so that they share one copy of the
-// chunk operands (W, K~^T, M, q) in LDS.
+// scan kernel: one work-group (7 waves) per (state slice, v-head, sequence).
+// The 128 value columns of a head's state form 8 slices of 16; columns
+// evolve independently, so each slice has its own serial chain and CU.
 //
-//   waves 0, 1  the chains of slices 2p and 2p+1: each keeps its 128x16 fp32
-//               state in registers and per chunk forms V_n = U - W S and
-//               S <- e^{c_63} S + K~^T V_n from a 3-stage LDS ring.
-//   waves 4-6   loaders: each moves a third of a chunk's operands (fragment
-//               ordered, 16 bytes per lane per fragment) into the ring.
-//   waves 2, 3, 7   output waves; the j-th forms O (32 columns) for chunks
+//   wave 0      the chain: keeps the slice's 128x16 fp32 state in registers
+//               and per chunk forms V_n = U - W S and S <- e^{c_63} S +
+//               K~^T V_n from a 3-stage LDS ring.
+//   waves 1-3   loaders: each moves a third of a chunk's operands (fragment
+//               ordered, 16 bytes per lane per fragment) from global memory
+//               into the ring.  The 8 slices of a head share id % 8 (one XCD,
+//               one L2), so each operand line comes from HBM once per XCD.
+//   waves 4-6   output waves; the j-th forms O (16 columns) for chunks
 //               c = j mod 3 from S_c and V_n handed over in LDS slot j, and
 //               writes it through a private LDS tile with 16-byte stores.
 //               Each issues its next chunk's loads before its stores, so it
@@ -648,28 +648,28 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 // Waves meet only through LDS counters with bounded waits, never through a
 // work-group barrier, so no wave waits on one it does not depend on.
 // ---------------------------------------------------------------------------
-constexpr int kPairs = 4;              // work-groups (slice pairs) per (sequence, head)
+constexpr int kSlicesPerHead = kDV / kBV;   // 8 work-groups per (sequence, head)
 constexpr int kRing = 3;               // operand stages
 constexpr int kHand = kOutWaves;       // hand-off slots: chunk c uses slot c % kHand (= its output wave)
 constexpr int kLoaders = 3;
 constexpr int kSpinLimit = 1 << 20;    // bounded waits: ~0.1 s, then the wave gives up
 
-// The 36 fragments of one chunk (W 0..15, K~^T 16..31, U of the two slices
-// 32..35), split over the loaders; fragment f sits at index f of a stage.
-constexpr int kStageFrags = 36;
-constexpr int kLoaderFrags[kLoaders + 1] = {0, 12, 24, 36};
+// The 34 fragments of one chunk (W 0..15, K~^T 16..31, the slice's U
+// 32..33), split over the loaders; fragment f sits at index f of a stage.
+constexpr int kStageFrags = 34;
+constexpr int kLoaderFrags[kLoaders + 1] = {0, 12, 24, 34};
 
 struct ScanSmem {
     half8 stage[kRing][kStageFrags][64];
     float gd[kRing];                       // e^{c_63} of the chunk in each stage
-    half8 hs[kHand][2][4][64];             // S at the start of a chunk, per chain, B-fragments
-    half8 hv[kHand][2][2][64];             // V_n, per chain, B-fragments
-    uint16_t ot[kOutWaves][kChunk][2 * kBV];   // output tiles (bf16), one per output wave
+    half8 hs[kHand][4][64];                // S at the start of a chunk, B-fragments
+    half8 hv[kHand][2][64];                // V_n, B-fragments
+    uint16_t ot[kOutWaves][kChunk][kBV];   // output tiles (bf16), one per output wave
     int filled[4];                         // per loader: chunks whose part sits in the ring
-    int freed[2];                          // per chain: chunks whose stage it has finished reading
-    int ready[2];                          // per chain: chunks whose hand-off part is written
+    int freed;                             // chunks whose stage the chain has finished reading
+    int ready;                             // chunks whose hand-off is written
     int cons[kHand];                       // per slot: 1 + the chunk an output wave last read from it
-    int red[kScanThreads / 64];
+    int red[(kScanThreads + 63) / 64];
 };
 
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
@@ -714,15 +714,6 @@ __device__ inline bool wait_chain(const ScanSmem& sm, int c, int slot) {
     return false;
 }
 
-__device__ inline bool wait_both(const int* flags, int target) {
-    for (int it = 0; it < kSpinLimit; ++it) {
-        const int a = lds_load_relaxed(flags), b = lds_load_relaxed(flags + 1);
-        if (min(a, b) >= target) return true;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return false;
-}
-
 // One loader wave (see the scan kernel): fragments kLoaderFrags[J] ..
 // kLoaderFrags[J+1] of every chunk, with compile-time fragment indices so
 // the loads and LDS writes are straight-line code; loader 2 also moves the
@@ -731,13 +722,13 @@ __device__ inline bool wait_both(const int* flags, int target) {
 // bounds) and are dropped.
 template <int J>
 __device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nch, int hv, int HV,
-                           int sp, int lane) {
+                           int sl, int lane) {
     constexpr int f0 = kLoaderFrags[J], nf = kLoaderFrags[J + 1] - kLoaderFrags[J];
     auto load = [&](int c, u32x4 (&fr)[nf], float& dg) {
         const size_t chh = (size_t)(chunk0 + min(c, nch - 1)) * HV + hv;
         const u32x4* wsrc = reinterpret_cast<const u32x4*>(ws.Wf + chh * kWfElems) + lane;
         const u32x4* ksrc = reinterpret_cast<const u32x4*>(ws.Kf + chh * kKfElems) + lane;
-        const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sp * 4 * 64 + lane;
+        const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sl * 2 * 64 + lane;
 #pragma unroll
         for (int i = 0; i < nf; ++i) {
             const int f = f0 + i;
@@ -746,7 +737,7 @@ __device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nc
         if (J == kLoaders - 1) dg = ws.gates[chh * kGateFloats + kGateDecay];
     };
     auto store = [&](int c, int st, const u32x4 (&fr)[nf], float dg) -> bool {
-        if (c >= kRing && !wait_both(sm.freed, c - kRing + 1)) return false;
+        if (c >= kRing && !wait_ge(&sm.freed, c - kRing + 1)) return false;
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int i = 0; i < nf; ++i) *reinterpret_cast<u32x4*>(&sm.stage[st][f0 + i][lane]) = fr[i];
@@ -782,12 +773,12 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
 
-    // XCD-aware id: the kPairs work-groups of one (seq, head) pair share id % 8
+    // XCD-aware id: the 8 slices of one (seq, head) pair share id % 8
     // (work-group i runs on XCD i % 8), so they read the head's operands from one L2
     const int id = blockIdx.x;
     const int xcd = id & 7, qd = id >> 3;
-    const int sp = qd & (kPairs - 1);
-    const int pair = (qd / kPairs) * 8 + xcd;
+    const int sl = qd & (kSlicesPerHead - 1);
+    const int pair = (qd / kSlicesPerHead) * 8 + xcd;
     if (pair >= N * HV) return;
     const int seq = pair / HV, hv = pair - seq * HV;
     const int hk = hv / (HV / HK);
@@ -798,16 +789,14 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     const int chunk0 = __builtin_amdgcn_readfirstlane(chunks_before<kScanThreads>(cu, T, seq, sm.red));
     if (tid < 4) lds_store_relaxed(&sm.filled[tid], 0);
     if (tid < 2) {
-        lds_store_relaxed(&sm.freed[tid], 0);
-        lds_store_relaxed(&sm.ready[tid], 0);
+        lds_store_relaxed(&sm.freed, 0);
+        lds_store_relaxed(&sm.ready, 0);
     }
     if (tid < kHand) lds_store_relaxed(&sm.cons[tid], 0);
     __syncthreads();
 
-    if (wave < 2) {
-        // ---------------- chain waves: slice 2 sp + h
-        const int h = wave;
-        const int sl = 2 * sp + h;
+    if (wave == 0) {
+        // ---------------- chain wave: slice sl
         const size_t sbase = ((size_t)seq * HV + hv) * kDK * kDV + sl * kBV + lm;
         f32x4 S[8];
         if (s0) {   // one uniform branch: all 32 loads in flight together
@@ -839,18 +828,18 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             // landed: publish both
             lds_wait_all();
             if (lane == 0 && c > 0) {
-                lds_store_relaxed(&sm.freed[h], c);
-                lds_store_relaxed(&sm.ready[h], c);
+                lds_store_relaxed(&sm.freed, c);
+                lds_store_relaxed(&sm.ready, c);
             }
             // S_c goes to the hand-off slot now: it is known before the
             // chunk's products
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) sm.hs[hslot][h][kb][lane] = sb[kb];
+            for (int kb = 0; kb < 4; ++kb) sm.hs[hslot][kb][lane] = sb[kb];
             const half8(&sg)[kStageFrags][64] = sm.stage[st];
             half8 wv[16], kv[16];
 #pragma unroll
             for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
-            const half8 u0 = sg[32 + 2 * h][lane], u1 = sg[33 + 2 * h][lane];
+            const half8 u0 = sg[32][lane], u1 = sg[33][lane];
             const float d = sm.gd[st];
 #pragma unroll
             for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
@@ -881,8 +870,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             half8 vb[2];
             vb[0] = cat8(to_half4(P[0]), to_half4(P[1]));
             vb[1] = cat8(to_half4(P[2]), to_half4(P[3]));
-            sm.hv[hslot][h][0][lane] = vb[0];
-            sm.hv[hslot][h][1][lane] = vb[1];
+            sm.hv[hslot][0][lane] = vb[0];
+            sm.hv[hslot][1][lane] = vb[1];
             // S = d S + K~^T V_n (128 x 16), k over tokens; eight independent
             // tiles, issued round-robin
 #pragma unroll
@@ -897,22 +886,22 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
         // the last chunk's stage reads and hand-off
         lds_wait_all();
         if (lane == 0 && ok) {
-            lds_store_relaxed(&sm.freed[h], nch);
-            lds_store_relaxed(&sm.ready[h], nch);
+            lds_store_relaxed(&sm.freed, nch);
+            lds_store_relaxed(&sm.ready, nch);
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sf[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV] = S[t][i];
         }
-    } else if (wave >= 4 && wave < 4 + kLoaders) {
-        const int j = wave - 4;
-        if (j == 0) run_loader<0>(sm, ws, chunk0, nch, hv, HV, sp, lane);
-        else if (j == 1) run_loader<1>(sm, ws, chunk0, nch, hv, HV, sp, lane);
-        else run_loader<2>(sm, ws, chunk0, nch, hv, HV, sp, lane);
+    } else if (wave <= kLoaders) {
+        const int j = wave - 1;
+        if (j == 0) run_loader<0>(sm, ws, chunk0, nch, hv, HV, sl, lane);
+        else if (j == 1) run_loader<1>(sm, ws, chunk0, nch, hv, HV, sl, lane);
+        else run_loader<2>(sm, ws, chunk0, nch, hv, HV, sl, lane);
     } else {
-        // ---------------- output waves (2, 3, 7): chunks c = ow, ow + kOutWaves, ...
-        const int ow = wave == 7 ? 2 : wave - 2;
+        // ---------------- output waves (4-6): chunks c = ow, ow + kOutWaves, ...
+        const int ow = wave - 1 - kLoaders;
         // operands of chunk c (clamped into range, so a look-ahead past the
         // end re-reads the last chunk): Q fragments (fp16, row tile mt,
         // k-block kb, from the GQA group's first v-head), s e^c of the
@@ -933,66 +922,57 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             for (int f = 0; f < 8; ++f) mf[f] = msrc[f * 64];
         };
         if (ow < nch) load_ops(ow);
-        uint16_t(&ot)[kChunk][2 * kBV] = sm.ot[ow];
+        uint16_t(&ot)[kChunk][kBV] = sm.ot[ow];
         for (int c = ow; c < nch; c += kOutWaves) {
             const int rows = min(kChunk, len - c * kChunk);
-            if (!wait_both(sm.ready, c + 1)) break;
+            if (!wait_ge(&sm.ready, c + 1)) break;
             asm volatile("" ::: "memory");
             const int slot = ow;   // c % kHand
-            half8 hsb[2][4], hvb[2][2];
+            half8 hsb[4], hvb[2];
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) hsb[s2][kb] = sm.hs[slot][s2][kb][lane];
-                hvb[s2][0] = sm.hv[slot][s2][0][lane];
-                hvb[s2][1] = sm.hv[slot][s2][1][lane];
-            }
+            for (int kb = 0; kb < 4; ++kb) hsb[kb] = sm.hs[slot][kb][lane];
+            hvb[0] = sm.hv[slot][0][lane];
+            hvb[1] = sm.hv[slot][1][lane];
             lds_wait_all();
             if (lane == 0) lds_store_relaxed(&sm.cons[slot], c + 1);
 
-            // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T for both slices (operands
-            // swapped so each lane holds four consecutive columns of one
-            // token, whose s e^c then scales them); each accumulator's
-            // dependent products are issued round-robin
-            f32x4 ov[2][4];
+            // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T (operands swapped so each
+            // lane holds four consecutive columns of one token, whose s e^c
+            // then scales them); the four accumulators' products are issued
+            // round-robin
+            f32x4 ov[4];
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
+            for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hsb[0], qf[mt * 4], zero4());
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hsb[s2][0], qf[mt * 4], zero4());
+            for (int kb = 1; kb < 4; ++kb) {
 #pragma unroll
-                for (int kb = 1; kb < 4; ++kb) {
+                for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hsb[kb], qf[mt * 4 + kb], ov[mt]);
+            }
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hsb[s2][kb], qf[mt * 4 + kb], ov[s2][mt]);
-                }
+            for (int mt = 0; mt < 4; ++mt) ov[mt] = ov[mt] * es[mt];
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = ov[s2][mt] * es[mt];
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hvb[s2][kb], mf[mt * 2 + kb], ov[s2][mt]);
-                }
+                for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hvb[kb], mf[mt * 2 + kb], ov[mt]);
             }
             load_ops(c + kOutWaves);   // the operand registers are free again
-            // O tile (64 rows x 32 columns, bf16) through LDS, then 16-byte
-            // stores: lane (g, l) holds token 16 mt + l, columns 16 s2 + 4g ..
-            // + 3 (one 8-byte write each); lane l then writes row l, four
+            // O tile (64 rows x 16 columns, bf16) through LDS, then 16-byte
+            // stores: lane (g, l) holds token 16 mt + l, columns 4g .. 4g+3
+            // (one 8-byte write each); lane l then writes row l, two
             // 8-column pieces
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-                    uint2 pk;
-                    pk.x = (uint32_t)f32_to_bf16_bits(ov[s2][mt][0]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][1]) << 16);
-                    pk.y = (uint32_t)f32_to_bf16_bits(ov[s2][mt][2]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][3]) << 16);
-                    *reinterpret_cast<uint2*>(&ot[mt * 16 + lm][s2 * kBV + 4 * lg]) = pk;
-                }
+            for (int mt = 0; mt < 4; ++mt) {
+                uint2 pk;
+                pk.x = (uint32_t)f32_to_bf16_bits(ov[mt][0]) | ((uint32_t)f32_to_bf16_bits(ov[mt][1]) << 16);
+                pk.y = (uint32_t)f32_to_bf16_bits(ov[mt][2]) | ((uint32_t)f32_to_bf16_bits(ov[mt][3]) << 16);
+                *reinterpret_cast<uint2*>(&ot[mt * 16 + lm][4 * lg]) = pk;
             }
             asm volatile("" ::: "memory");   // LDS ops of one wave complete in order
             if (lane < rows) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(&ot[lane][0]);
-                u32x4* dst = reinterpret_cast<u32x4*>(o + ((size_t)(tok0 + c * kChunk + lane) * HV + hv) * kDV + 2 * sp * kBV);
-#pragma unroll
-                for (int p4 = 0; p4 < 4; ++p4) dst[p4] = src[p4];
+                u32x4* dst = reinterpret_cast<u32x4*>(o + ((size_t)(tok0 + c * kChunk + lane) * HV + hv) * kDV + sl * kBV);
+                dst[0] = src[0];
+                dst[1] = src[1];
             }
         }
     }
@@ -1036,7 +1016,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     if (only == 0) return hipSuccess;
     const int pairs = N * HV;
     const int groups = (pairs + 7) / 8;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 8 * kPairs)), dim3(kScanThreads), 0, stream,
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 8 * kSlicesPerHead)), dim3(kScanThreads), 0, stream,
                        ws, static_cast<const uint16_t*>(q), static_cast<uint16_t*>(o), s0, sf, cu,
                        N, T, HV, HK);
     hipError_t err = hipGetLastError();
