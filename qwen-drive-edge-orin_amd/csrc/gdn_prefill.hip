@@ -813,36 +813,51 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
 
-        bool ok = true;
-        int st = 0;      // stage of chunk c
-        int hslot = 0;   // hand-off slot of chunk c
+        // Software pipeline: chunk c + 1's W, U and decay are read from the
+        // ring while chunk c's V_n is formed, its K~^T while the state update
+        // runs, so the serial chain -W S + U -> V_n -> S waits on the matrix
+        // cores, not on LDS.
+        half8 wv[16], kv[16], u0, u1;
+        float d = 0.f;
+        auto read_w = [&](int st) {
+            const half8(&sg)[kStageFrags][64] = sm.stage[st];
+#pragma unroll
+            for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
+            u0 = sg[32][lane];
+            u1 = sg[33][lane];
+            d = sm.gd[st];
+        };
+        auto read_k = [&](int st) {
+            const half8(&sg)[kStageFrags][64] = sm.stage[st];
+#pragma unroll
+            for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
+        };
         // counters polled during the previous chunk (monotonic, so values
         // that already satisfy a wait let the chain skip the wait)
         int pf0 = 0, pf1 = 0, pf2 = 0, pfc = 0;
-        for (int c = 0; c < nch && ok; ++c) {
-            // chunk c's operands are in the ring and its hand-off slot is
-            // free (its previous chunk, c - kHand, was read)
+        // chunk c's operands are in the ring and its hand-off slot is free
+        // (its previous chunk, c - kHand, was read)
+        auto ensure = [&](int c, int slot) -> bool {
             const int cons_need = c >= kHand ? c - kHand + 1 : 0;
-            if (min(pf0, min(pf1, pf2)) < c + 1 || pfc < cons_need) ok = ok && wait_chain(sm, c, hslot);
-            // the previous chunk's stage reads and hand-off writes have
-            // landed: publish both
-            lds_wait_all();
-            if (lane == 0 && c > 0) {
-                lds_store_relaxed(&sm.freed, c);
-                lds_store_relaxed(&sm.ready, c);
-            }
+            if (min(pf0, min(pf1, pf2)) >= c + 1 && pfc >= cons_need) return true;
+            return wait_chain(sm, c, slot);
+        };
+        bool ok = nch > 0 && ensure(0, 0);
+        if (ok) {
+            asm volatile("" ::: "memory");
+            read_w(0);
+            read_k(0);
+        }
+        int st = 0;      // stage of chunk c
+        int hslot = 0;   // hand-off slot of chunk c
+        for (int c = 0; c < nch && ok; ++c) {
+            const int stn = (st == kRing - 1) ? 0 : st + 1;
+            const int hsn = (hslot == kHand - 1) ? 0 : hslot + 1;
+            const bool more = c + 1 < nch;
             // S_c goes to the hand-off slot now: it is known before the
             // chunk's products
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) sm.hs[hslot][kb][lane] = sb[kb];
-            const half8(&sg)[kStageFrags][64] = sm.stage[st];
-            half8 wv[16], kv[16];
-#pragma unroll
-            for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
-            const half8 u0 = sg[32][lane], u1 = sg[33][lane];
-            const float d = sm.gd[st];
-#pragma unroll
-            for (int f = 0; f < 16; ++f) kv[f] = sg[16 + f][lane];
             // V_n = U - W S (64 x 16): the stored -W accumulates onto U; k
             // over dk, the four row tiles independent and issued round-robin
             f32x4 P[4];
@@ -858,15 +873,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(wv[mt * 4 + kb], sb[kb], P[mt]);
             }
-            // the next chunk's counters, read while the products run
-            const int hsn = (hslot == kHand - 1) ? 0 : hslot + 1;
-            pf0 = lds_load_relaxed(&sm.filled[0]);
-            pf1 = lds_load_relaxed(&sm.filled[1]);
-            pf2 = lds_load_relaxed(&sm.filled[2]);
-            pfc = lds_load_relaxed(&sm.cons[hsn]);
+            const float dc = d;
+            // chunk c + 1's W, U and decay while the products run
+            if (more) {
+                ok = ok && ensure(c + 1, hsn);
+                asm volatile("" ::: "memory");
+                read_w(stn);
+            }
             // independent of P: the decayed state
 #pragma unroll
-            for (int t = 0; t < 8; ++t) S[t] = S[t] * d;
+            for (int t = 0; t < 8; ++t) S[t] = S[t] * dc;
             half8 vb[2];
             vb[0] = cat8(to_half4(P[0]), to_half4(P[1]));
             vb[1] = cat8(to_half4(P[2]), to_half4(P[3]));
@@ -878,16 +894,22 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 0], vb[0], S[t]);
 #pragma unroll
             for (int t = 0; t < 8; ++t) S[t] = mfma16(kv[t * 2 + 1], vb[1], S[t]);
-            hslot = hsn;
+            // stage st is read and chunk c's hand-off written: publish both,
+            // then chunk c + 1's K~^T while the update runs
+            lds_wait_all();
+            if (lane == 0) {
+                lds_store_relaxed(&sm.freed, c + 1);
+                lds_store_relaxed(&sm.ready, c + 1);
+            }
+            if (more) read_k(stn);
+            pf0 = lds_load_relaxed(&sm.filled[0]);
+            pf1 = lds_load_relaxed(&sm.filled[1]);
+            pf2 = lds_load_relaxed(&sm.filled[2]);
+            pfc = lds_load_relaxed(&sm.cons[(hsn == kHand - 1) ? 0 : hsn + 1]);
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) sb[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
-            st = (st == kRing - 1) ? 0 : st + 1;
-        }
-        // the last chunk's stage reads and hand-off
-        lds_wait_all();
-        if (lane == 0 && ok) {
-            lds_store_relaxed(&sm.freed, nch);
-            lds_store_relaxed(&sm.ready, nch);
+            st = stn;
+            hslot = hsn;
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
