@@ -42,8 +42,9 @@ namespace {
 
 constexpr int kPrepThreads = 256;
 // scan work-group: wave 0 runs the chain of one state slice, waves 1-3 load
-// its operands, waves 4-6 form outputs
-constexpr int kScanThreads = 448;
+// its operands, waves 5-7 form outputs (wave 4 only fills the group, so the
+// chain has its SIMD to itself)
+constexpr int kScanThreads = 512;
 constexpr int kOutWaves = 3;
 
 // Per chunk-head record sizes (elements)
@@ -629,7 +630,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (7 waves) per (state slice, v-head, sequence).
+// scan kernel: one work-group (8 waves) per (state slice, v-head, sequence).
 // The 128 value columns of a head's state form 8 slices of 16; columns
 // evolve independently, so each slice has its own serial chain and CU.
 //
@@ -640,7 +641,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 //               ordered, 16 bytes per lane per fragment) from global memory
 //               into the ring.  The 8 slices of a head share id % 8 (one XCD,
 //               one L2), so each operand line comes from HBM once per XCD.
-//   waves 4-6   output waves; the j-th forms O (16 columns) for chunks
+//   waves 5-7   output waves; the j-th forms O (16 columns) for chunks
 //               c = j mod 3 from S_c and V_n handed over in LDS slot j, and
 //               writes it through a private LDS tile with 16-byte stores.
 //               Each issues its next chunk's loads before its stores, so it
@@ -916,6 +917,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) sf[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV] = S[t][i];
         }
+    } else if (wave == kLoaders + 1) {
+        // idle: waves w and w + 4 share a SIMD, so no other wave runs beside the chain
     } else if (wave <= kLoaders) {
         const int j = wave - 1;
         if (j == 0) run_loader<0>(sm, ws, chunk0, nch, hv, HV, sl, lane);
@@ -923,7 +926,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
         else run_loader<2>(sm, ws, chunk0, nch, hv, HV, sl, lane);
     } else {
         // ---------------- output waves (4-6): chunks c = ow, ow + kOutWaves, ...
-        const int ow = wave - 1 - kLoaders;
+        const int ow = wave - 2 - kLoaders;
         // operands of chunk c (clamped into range, so a look-ahead past the
         // end re-reads the last chunk): Q fragments (fp16, row tile mt,
         // k-block kb, from the GQA group's first v-head), s e^c of the
