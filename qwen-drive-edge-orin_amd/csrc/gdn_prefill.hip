@@ -309,6 +309,18 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
             raw[ii] = *reinterpret_cast<const u32x4*>(base + (size_t)r * HK * kDK);
         }
     }
+    // this wave's Q rows (k-map over dk); bf16 straight into the MFMA.
+    // They are needed right after K, V only at the end: Q is loaded first
+    uint2 qr[4][2];
+    {
+        const uint16_t* qs =
+            q + ((size_t)(tok0 + min(wave * 16 + lm, rows - 1)) * HK + hk) * kDK + 4 * lg;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            qr[kb][0] = *reinterpret_cast<const uint2*>(qs + kb * 32);
+            qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
+        }
+    }
     // this wave's V rows for value columns 32 w .. 32 w + 31 (the U slices
     // 2w, 2w+1), k-mapped like an A operand: token tile tt, row 16 tt + lm
     uint2 vr[4][2];
@@ -319,17 +331,6 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
             const uint16_t* vrow = vs + (size_t)(tok0 + min(16 * tt + lm, rows - 1)) * HV * kDV;
             vr[tt][0] = *reinterpret_cast<const uint2*>(vrow);
             vr[tt][1] = *reinterpret_cast<const uint2*>(vrow + 16);
-        }
-    }
-    // this wave's Q rows (k-map over dk); bf16 straight into the MFMA
-    uint2 qr[4][2];
-    {
-        const uint16_t* qs =
-            q + ((size_t)(tok0 + min(wave * 16 + lm, rows - 1)) * HK + hk) * kDK + 4 * lg;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            qr[kb][0] = *reinterpret_cast<const uint2*>(qs + kb * 32);
-            qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
         }
     }
 
