@@ -41,9 +41,7 @@ namespace gdn {
 namespace {
 
 constexpr int kPrepThreads = 256;
-// scan work-group: wave 0 runs the chain of one state slice, waves 1-3 load
-// its operands, waves 5-7 form outputs (wave 4 only fills the group, so the
-// chain has its SIMD to itself)
+// scan work-group: 8 waves (chains, loaders, output waves; see the scan kernel)
 constexpr int kScanThreads = 512;
 constexpr int kOutWaves = 3;
 
@@ -631,47 +629,62 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (8 waves) per (state slice, v-head, sequence).
-// The 128 value columns of a head's state form 8 slices of 16; columns
-// evolve independently, so each slice has its own serial chain and CU.
+// scan kernel: one work-group (8 waves) per (SPW state slices, v-head,
+// sequence).  The 128 value columns of a head's state form 8 slices of 16;
+// columns evolve independently, so each slice has its own serial chain.
+// SPW = 1 gives every slice its own CU (small grids: B = 1 fills the chip
+// with 256 groups); SPW = 2 lets two chains share one copy of the chunk
+// operands, twice the work per CU for grids larger than the chip.
 //
-//   wave 0      the chain: keeps the slice's 128x16 fp32 state in registers
-//               and per chunk forms V_n = U - W S and S <- e^{c_63} S +
-//               K~^T V_n from a 3-stage LDS ring.
-//   waves 1-3   loaders: each moves a third of a chunk's operands (fragment
-//               ordered, 16 bytes per lane per fragment) from global memory
-//               into the ring.  The 8 slices of a head share id % 8 (one XCD,
-//               one L2), so each operand line comes from HBM once per XCD.
-//   waves 5-7   output waves; the j-th forms O (16 columns) for chunks
+//   chains      wave h < SPW keeps slice SPW*p + h's 128x16 fp32 state in
+//               registers and per chunk forms V_n = U - W S and
+//               S <- e^{c_63} S + K~^T V_n from a 3-stage LDS ring, reading
+//               the next chunk's operands while the current products run.
+//   loaders     three waves; each moves a third of a chunk's operands
+//               (fragment ordered, 16 bytes per lane per fragment) from
+//               global memory into the ring.  The groups of one head share
+//               id % 8 (one XCD, one L2), so each operand line comes from
+//               HBM once per XCD.
+//   outputs     three waves; the j-th forms O (16 SPW columns) for chunks
 //               c = j mod 3 from S_c and V_n handed over in LDS slot j, and
 //               writes it through a private LDS tile with 16-byte stores.
 //               Each issues its next chunk's loads before its stores, so it
 //               never waits for its own stores to complete.
-// Waves meet only through LDS counters with bounded waits, never through a
-// work-group barrier, so no wave waits on one it does not depend on.
+// Wave roles (waves w and w + 4 share a SIMD): SPW = 1: chain 0, loaders
+// 1-3, wave 4 idle (the chain keeps its SIMD to itself), outputs 5-7;
+// SPW = 2: chains 0-1, outputs 2, 3, 7, loaders 4-6.  Waves meet only
+// through LDS counters with bounded waits, never through a work-group
+// barrier, so no wave waits on one it does not depend on.
 // ---------------------------------------------------------------------------
-constexpr int kSlicesPerHead = kDV / kBV;   // 8 work-groups per (sequence, head)
+constexpr int kSlicesPerHead = kDV / kBV;   // 8
 constexpr int kRing = 3;               // operand stages
 constexpr int kHand = kOutWaves;       // hand-off slots: chunk c uses slot c % kHand (= its output wave)
 constexpr int kLoaders = 3;
 constexpr int kSpinLimit = 1 << 20;    // bounded waits: ~0.1 s, then the wave gives up
 
-// The 34 fragments of one chunk (W 0..15, K~^T 16..31, the slice's U
-// 32..33), split over the loaders; fragment f sits at index f of a stage.
-constexpr int kStageFrags = 34;
-constexpr int kLoaderFrags[kLoaders + 1] = {0, 12, 24, 34};
+// Fragments of one chunk: W 0..15, K~^T 16..31, then U of each slice (2
+// each); split over the loaders, fragment f sits at index f of a stage.
+template <int SPW>
+struct ScanCfg {
+    static constexpr int kStageFrags = 32 + 2 * SPW;
+    static constexpr int kLoaderBegin[kLoaders + 1] = {0, 12, 24, kStageFrags};
+    static constexpr int kGroupsPerHead = kSlicesPerHead / SPW;
+    static __device__ int loader_of(int wave) { return SPW == 1 ? wave - 1 : wave - 4; }   // -1 .. : not a loader
+    static __device__ int output_of(int wave) { return SPW == 1 ? wave - 5 : (wave == 7 ? 2 : wave - 2); }
+};
 
+template <int SPW>
 struct ScanSmem {
-    half8 stage[kRing][kStageFrags][64];
+    half8 stage[kRing][ScanCfg<SPW>::kStageFrags][64];
     float gd[kRing];                       // e^{c_63} of the chunk in each stage
-    half8 hs[kHand][4][64];                // S at the start of a chunk, B-fragments
-    half8 hv[kHand][2][64];                // V_n, B-fragments
-    uint16_t ot[kOutWaves][kChunk][kBV];   // output tiles (bf16), one per output wave
+    half8 hs[kHand][SPW][4][64];           // S at the start of a chunk, per chain, B-fragments
+    half8 hv[kHand][SPW][2][64];           // V_n, per chain, B-fragments
+    uint16_t ot[kOutWaves][kChunk][SPW * kBV];   // output tiles (bf16), one per output wave
     int filled[4];                         // per loader: chunks whose part sits in the ring
-    int freed;                             // chunks whose stage the chain has finished reading
-    int ready;                             // chunks whose hand-off is written
+    int freed[SPW];                        // per chain: chunks whose stage it has finished reading
+    int ready[SPW];                        // per chain: chunks whose hand-off part is written
     int cons[kHand];                       // per slot: 1 + the chunk an output wave last read from it
-    int red[(kScanThreads + 63) / 64];
+    int red[kScanThreads / 64];
 };
 
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
@@ -701,10 +714,30 @@ __device__ inline bool wait_ge(const int* flag, int target) {
     return false;
 }
 
+// Smallest of n counters (LDS reads issued together).
+template <int n>
+__device__ inline int lds_min(const int* p) {
+    int m = lds_load_relaxed(p);
+#pragma unroll
+    for (int i = 1; i < n; ++i) m = min(m, lds_load_relaxed(p + i));
+    return m;
+}
+
+// Wait (bounded) until the smallest of n counters is >= target.
+template <int n>
+__device__ inline bool wait_min(const int* p, int target) {
+    for (int it = 0; it < kSpinLimit; ++it) {
+        if (lds_min<n>(p) >= target) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
 // Wait (bounded) until every loader has put chunk c in the ring and the
 // hand-off slot of chunk c is free (the output wave read chunk c - kHand);
 // the four LDS reads of a poll are issued together.
-__device__ inline bool wait_chain(const ScanSmem& sm, int c, int slot) {
+template <int SPW>
+__device__ inline bool wait_chain(const ScanSmem<SPW>& sm, int c, int slot) {
     static_assert(kLoaders == 3, "three loader counters");
     const int cons_need = c >= kHand ? c - kHand + 1 : 0;
     for (int it = 0; it < kSpinLimit; ++it) {
@@ -716,21 +749,22 @@ __device__ inline bool wait_chain(const ScanSmem& sm, int c, int slot) {
     return false;
 }
 
-// One loader wave (see the scan kernel): fragments kLoaderFrags[J] ..
-// kLoaderFrags[J+1] of every chunk, with compile-time fragment indices so
+// One loader wave (see the scan kernel): fragments kLoaderBegin[J] ..
+// kLoaderBegin[J+1] of every chunk, with compile-time fragment indices so
 // the loads and LDS writes are straight-line code; loader 2 also moves the
 // decay.  Two chunks are in flight: chunk c+1's loads are issued before
 // chunk c is written.  Loads past the last chunk re-read it (always in
 // bounds) and are dropped.
-template <int J>
-__device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nch, int hv, int HV,
-                           int sl, int lane) {
-    constexpr int f0 = kLoaderFrags[J], nf = kLoaderFrags[J + 1] - kLoaderFrags[J];
+template <int SPW, int J>
+__device__ void run_loader(ScanSmem<SPW>& sm, const Workspace& ws, int chunk0, int nch, int hv,
+                           int HV, int sl0, int lane) {
+    constexpr int f0 = ScanCfg<SPW>::kLoaderBegin[J];
+    constexpr int nf = ScanCfg<SPW>::kLoaderBegin[J + 1] - f0;
     auto load = [&](int c, u32x4 (&fr)[nf], float& dg) {
         const size_t chh = (size_t)(chunk0 + min(c, nch - 1)) * HV + hv;
         const u32x4* wsrc = reinterpret_cast<const u32x4*>(ws.Wf + chh * kWfElems) + lane;
         const u32x4* ksrc = reinterpret_cast<const u32x4*>(ws.Kf + chh * kKfElems) + lane;
-        const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sl * 2 * 64 + lane;
+        const u32x4* usrc = reinterpret_cast<const u32x4*>(ws.Uf + chh * kUfElems) + sl0 * 2 * 64 + lane;
 #pragma unroll
         for (int i = 0; i < nf; ++i) {
             const int f = f0 + i;
@@ -739,7 +773,7 @@ __device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nc
         if (J == kLoaders - 1) dg = ws.gates[chh * kGateFloats + kGateDecay];
     };
     auto store = [&](int c, int st, const u32x4 (&fr)[nf], float dg) -> bool {
-        if (c >= kRing && !wait_ge(&sm.freed, c - kRing + 1)) return false;
+        if (c >= kRing && !wait_min<SPW>(sm.freed, c - kRing + 1)) return false;
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int i = 0; i < nf; ++i) *reinterpret_cast<u32x4*>(&sm.stage[st][f0 + i][lane]) = fr[i];
@@ -763,43 +797,47 @@ __device__ void run_loader(ScanSmem& sm, const Workspace& ws, int chunk0, int nc
             st = (st == kRing - 1) ? 0 : st + 1;
         }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+template <int SPW>
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
-    Workspace ws, const uint16_t* __restrict__ q, uint16_t* __restrict__ o,
-    const float* __restrict__ s0, float* __restrict__ sf, const int32_t* __restrict__ cu, int N,
-    int T, int HV, int HK) {
-    __shared__ ScanSmem sm;
+    Workspace ws, uint16_t* __restrict__ o, const float* __restrict__ s0, float* __restrict__ sf,
+    const int32_t* __restrict__ cu, int N, int T, int HV, int HK) {
+    using Cfg = ScanCfg<SPW>;
+    constexpr int kStageFrags = Cfg::kStageFrags;
+    __shared__ ScanSmem<SPW> sm;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
 
-    // XCD-aware id: the 8 slices of one (seq, head) pair share id % 8
-    // (work-group i runs on XCD i % 8), so they read the head's operands from one L2
+    // XCD-aware id: the groups of one (seq, head) pair share id % 8 (work-group
+    // i runs on XCD i % 8), so they read the head's operands from one L2
     const int id = blockIdx.x;
     const int xcd = id & 7, qd = id >> 3;
-    const int sl = qd & (kSlicesPerHead - 1);
-    const int pair = (qd / kSlicesPerHead) * 8 + xcd;
+    const int sp = qd % Cfg::kGroupsPerHead;
+    const int pair = (qd / Cfg::kGroupsPerHead) * 8 + xcd;
     if (pair >= N * HV) return;
     const int seq = pair / HV, hv = pair - seq * HV;
     const int hk = hv / (HV / HK);
+    const int sl0 = SPW * sp;   // first slice of this group
 
     const int len = seq_len(cu, T, seq);
     const int tok0 = seq_start(cu, T, seq);
     const int nch = (len + kChunk - 1) / kChunk;
     const int chunk0 = __builtin_amdgcn_readfirstlane(chunks_before<kScanThreads>(cu, T, seq, sm.red));
     if (tid < 4) lds_store_relaxed(&sm.filled[tid], 0);
-    if (tid < 2) {
-        lds_store_relaxed(&sm.freed, 0);
-        lds_store_relaxed(&sm.ready, 0);
+    if (tid < SPW) {
+        lds_store_relaxed(&sm.freed[tid], 0);
+        lds_store_relaxed(&sm.ready[tid], 0);
     }
     if (tid < kHand) lds_store_relaxed(&sm.cons[tid], 0);
     __syncthreads();
 
-    if (wave == 0) {
-        // ---------------- chain wave: slice sl
-        const size_t sbase = ((size_t)seq * HV + hv) * kDK * kDV + sl * kBV + lm;
+    const int li = Cfg::loader_of(wave), oi = Cfg::output_of(wave);
+    if (wave < SPW) {
+        // ---------------- chain wave h: slice sl0 + h
+        const int h = wave;
+        const size_t sbase = ((size_t)seq * HV + hv) * kDK * kDV + (sl0 + h) * kBV + lm;
         f32x4 S[8];
         if (s0) {   // one uniform branch: all 32 loads in flight together
 #pragma unroll
@@ -825,8 +863,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             const half8(&sg)[kStageFrags][64] = sm.stage[st];
 #pragma unroll
             for (int f = 0; f < 16; ++f) wv[f] = sg[f][lane];
-            u0 = sg[32][lane];
-            u1 = sg[33][lane];
+            u0 = sg[32 + 2 * h][lane];
+            u1 = sg[33 + 2 * h][lane];
             d = sm.gd[st];
         };
         auto read_k = [&](int st) {
@@ -842,7 +880,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
         auto ensure = [&](int c, int slot) -> bool {
             const int cons_need = c >= kHand ? c - kHand + 1 : 0;
             if (min(pf0, min(pf1, pf2)) >= c + 1 && pfc >= cons_need) return true;
-            return wait_chain(sm, c, slot);
+            return wait_chain<SPW>(sm, c, slot);
         };
         bool ok = nch > 0 && ensure(0, 0);
         if (ok) {
@@ -859,7 +897,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             // S_c goes to the hand-off slot now: it is known before the
             // chunk's products
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) sm.hs[hslot][kb][lane] = sb[kb];
+            for (int kb = 0; kb < 4; ++kb) sm.hs[hslot][h][kb][lane] = sb[kb];
             // V_n = U - W S (64 x 16): the stored -W accumulates onto U; k
             // over dk, the four row tiles independent and issued round-robin
             f32x4 P[4];
@@ -888,8 +926,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             half8 vb[2];
             vb[0] = cat8(to_half4(P[0]), to_half4(P[1]));
             vb[1] = cat8(to_half4(P[2]), to_half4(P[3]));
-            sm.hv[hslot][0][lane] = vb[0];
-            sm.hv[hslot][1][lane] = vb[1];
+            sm.hv[hslot][h][0][lane] = vb[0];
+            sm.hv[hslot][h][1][lane] = vb[1];
             // S = d S + K~^T V_n (128 x 16), k over tokens; eight independent
             // tiles, issued round-robin
 #pragma unroll
@@ -900,8 +938,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             // then chunk c + 1's K~^T while the update runs
             lds_wait_all();
             if (lane == 0) {
-                lds_store_relaxed(&sm.freed, c + 1);
-                lds_store_relaxed(&sm.ready, c + 1);
+                lds_store_relaxed(&sm.freed[h], c + 1);
+                lds_store_relaxed(&sm.ready[h], c + 1);
             }
             if (more) read_k(stn);
             pf0 = lds_load_relaxed(&sm.filled[0]);
@@ -918,16 +956,13 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) sf[sbase + (size_t)(t * 16 + 4 * lg + i) * kDV] = S[t][i];
         }
-    } else if (wave == kLoaders + 1) {
-        // idle: waves w and w + 4 share a SIMD, so no other wave runs beside the chain
-    } else if (wave <= kLoaders) {
-        const int j = wave - 1;
-        if (j == 0) run_loader<0>(sm, ws, chunk0, nch, hv, HV, sl, lane);
-        else if (j == 1) run_loader<1>(sm, ws, chunk0, nch, hv, HV, sl, lane);
-        else run_loader<2>(sm, ws, chunk0, nch, hv, HV, sl, lane);
-    } else {
-        // ---------------- output waves (4-6): chunks c = ow, ow + kOutWaves, ...
-        const int ow = wave - 2 - kLoaders;
+    } else if (li >= 0 && li < kLoaders) {
+        if (li == 0) run_loader<SPW, 0>(sm, ws, chunk0, nch, hv, HV, sl0, lane);
+        else if (li == 1) run_loader<SPW, 1>(sm, ws, chunk0, nch, hv, HV, sl0, lane);
+        else run_loader<SPW, 2>(sm, ws, chunk0, nch, hv, HV, sl0, lane);
+    } else if (oi >= 0 && oi < kOutWaves) {
+        // ---------------- output waves: chunks c = ow, ow + kOutWaves, ...
+        const int ow = oi;
         // operands of chunk c (clamped into range, so a look-ahead past the
         // end re-reads the last chunk): Q fragments (fp16, row tile mt,
         // k-block kb, from the GQA group's first v-head), s e^c of the
@@ -948,60 +983,71 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             for (int f = 0; f < 8; ++f) mf[f] = msrc[f * 64];
         };
         if (ow < nch) load_ops(ow);
-        uint16_t(&ot)[kChunk][kBV] = sm.ot[ow];
+        uint16_t(&ot)[kChunk][SPW * kBV] = sm.ot[ow];
         for (int c = ow; c < nch; c += kOutWaves) {
             const int rows = min(kChunk, len - c * kChunk);
-            if (!wait_ge(&sm.ready, c + 1)) break;
+            if (!wait_min<SPW>(sm.ready, c + 1)) break;
             asm volatile("" ::: "memory");
             const int slot = ow;   // c % kHand
-            half8 hsb[4], hvb[2];
+            half8 hsb[SPW][4], hvb[SPW][2];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) hsb[kb] = sm.hs[slot][kb][lane];
-            hvb[0] = sm.hv[slot][0][lane];
-            hvb[1] = sm.hv[slot][1][lane];
+            for (int s2 = 0; s2 < SPW; ++s2) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) hsb[s2][kb] = sm.hs[slot][s2][kb][lane];
+                hvb[s2][0] = sm.hv[slot][s2][0][lane];
+                hvb[s2][1] = sm.hv[slot][s2][1][lane];
+            }
             lds_wait_all();
             if (lane == 0) lds_store_relaxed(&sm.cons[slot], c + 1);
 
-            // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T (operands swapped so each
-            // lane holds four consecutive columns of one token, whose s e^c
-            // then scales them); the four accumulators' products are issued
-            // round-robin
-            f32x4 ov[4];
+            // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T per slice (operands
+            // swapped so each lane holds four consecutive columns of one
+            // token, whose s e^c then scales them); each accumulator's
+            // dependent products are issued round-robin
+            f32x4 ov[SPW][4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hsb[0], qf[mt * 4], zero4());
+            for (int s2 = 0; s2 < SPW; ++s2) {
 #pragma unroll
-            for (int kb = 1; kb < 4; ++kb) {
+                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hsb[s2][0], qf[mt * 4], zero4());
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hsb[kb], qf[mt * 4 + kb], ov[mt]);
-            }
+                for (int kb = 1; kb < 4; ++kb) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) ov[mt] = ov[mt] * es[mt];
+                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hsb[s2][kb], qf[mt * 4 + kb], ov[s2][mt]);
+                }
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = ov[s2][mt] * es[mt];
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hvb[kb], mf[mt * 2 + kb], ov[mt]);
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) ov[s2][mt] = mfma16(hvb[s2][kb], mf[mt * 2 + kb], ov[s2][mt]);
+                }
             }
             load_ops(c + kOutWaves);   // the operand registers are free again
-            // O tile (64 rows x 16 columns, bf16) through LDS, then 16-byte
-            // stores: lane (g, l) holds token 16 mt + l, columns 4g .. 4g+3
-            // (one 8-byte write each); lane l then writes row l, two
+            // O tile (64 rows x 16 SPW columns, bf16) through LDS, then 16-byte
+            // stores: lane (g, l) holds token 16 mt + l, columns 16 s2 + 4g ..
+            // + 3 (one 8-byte write each); lane l then writes row l in
             // 8-column pieces
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                uint2 pk;
-                pk.x = (uint32_t)f32_to_bf16_bits(ov[mt][0]) | ((uint32_t)f32_to_bf16_bits(ov[mt][1]) << 16);
-                pk.y = (uint32_t)f32_to_bf16_bits(ov[mt][2]) | ((uint32_t)f32_to_bf16_bits(ov[mt][3]) << 16);
-                *reinterpret_cast<uint2*>(&ot[mt * 16 + lm][4 * lg]) = pk;
+            for (int s2 = 0; s2 < SPW; ++s2) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    uint2 pk;
+                    pk.x = (uint32_t)f32_to_bf16_bits(ov[s2][mt][0]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][1]) << 16);
+                    pk.y = (uint32_t)f32_to_bf16_bits(ov[s2][mt][2]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][3]) << 16);
+                    *reinterpret_cast<uint2*>(&ot[mt * 16 + lm][s2 * kBV + 4 * lg]) = pk;
+                }
             }
             asm volatile("" ::: "memory");   // LDS ops of one wave complete in order
             if (lane < rows) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(&ot[lane][0]);
-                u32x4* dst = reinterpret_cast<u32x4*>(o + ((size_t)(tok0 + c * kChunk + lane) * HV + hv) * kDV + sl * kBV);
-                dst[0] = src[0];
-                dst[1] = src[1];
+                u32x4* dst = reinterpret_cast<u32x4*>(o + ((size_t)(tok0 + c * kChunk + lane) * HV + hv) * kDV + sl0 * kBV);
+#pragma unroll
+                for (int p4 = 0; p4 < 2 * SPW; ++p4) dst[p4] = src[p4];
             }
         }
     }
+    // any other wave (SPW = 1: wave 4) is idle: waves w and w + 4 share a
+    // SIMD, so the chain keeps its SIMD to itself
 }
 
 hipError_t launch_prefill(const void* q, const void* k, const void* v, const float* g,
@@ -1040,11 +1086,22 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     }
     if (ev) (void)hipEventRecord(ev[1], stream);
     if (only == 0) return hipSuccess;
+    // one slice per work-group while that still fits the chip in one pass,
+    // else two (twice the work per CU)
     const int pairs = N * HV;
     const int groups = (pairs + 7) / 8;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)(groups * 8 * kSlicesPerHead)), dim3(kScanThreads), 0, stream,
-                       ws, static_cast<const uint16_t*>(q), static_cast<uint16_t*>(o), s0, sf, cu,
-                       N, T, HV, HK);
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 0;   // unknown: two slices per group
+    if ((long)groups * 8 * kSlicesPerHead <= (long)cus)
+        hipLaunchKernelGGL(gdn_scan_kernel<1>, dim3((unsigned)(groups * 8 * ScanCfg<1>::kGroupsPerHead)),
+                           dim3(kScanThreads), 0, stream, ws, static_cast<uint16_t*>(o), s0, sf, cu,
+                           N, T, HV, HK);
+    else
+        hipLaunchKernelGGL(gdn_scan_kernel<2>, dim3((unsigned)(groups * 8 * ScanCfg<2>::kGroupsPerHead)),
+                           dim3(kScanThreads), 0, stream, ws, static_cast<uint16_t*>(o), s0, sf, cu,
+                           N, T, HV, HK);
     hipError_t err = hipGetLastError();
     if (ev) (void)hipEventRecord(ev[2], stream);
     return err;
