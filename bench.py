@@ -8,7 +8,8 @@ HK=16, d=128, bf16 inputs, fp32 state, synthetic seeded data.  Inputs are
 resident in HBM before timing starts; successive steps rotate through enough
 input copies (> 256 MB) that the Infinity Cache cannot serve them, so the
 timed number is the cold one.  The warm (same inputs every step) number and
-the secondary workloads (gated RMSNorm, decode step, varlen prefill) are
+the secondary workloads (gated RMSNorm, decode step, varlen prefill, causal
+conv1d prefill and decode update) are
 reported in the same JSON line.
 
 Prints ONE JSON line.  `value` is TFLOP/s under the fixed dense FLOP
@@ -143,6 +144,35 @@ def bench_norm(ops, dev, steps, warmup):
                     len(sets), max(4, steps // len(sets)), warmup)
     algo = per + _bytes(x)
     return dict(ms=ms, gbs=algo / ms / 1e6, frac=algo / ms / 1e6 / HBM_PEAK_GBS, bytes=algo)
+
+
+def bench_conv(ops, dev, steps, warmup):
+    """Causal conv1d + SiLU ahead of the recurrence: the prefill form over
+    the layer's conv channels (D = 2 * 16 * 128 + 32 * 128 = 8192, T = 1141,
+    K = 4, bf16) and the decode update at B = 64 (state of 4 tokens)."""
+    import torch
+
+    D, T, K = 8192, 1141, 4
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(1, T, D, generator=gen).bfloat16()
+    w = (0.5 * torch.randn(D, K, generator=gen)).bfloat16()
+    per = _bytes(x)
+    sets = rotation(lambda: (x, w), per, dev)
+    ms = time_graph(lambda i: ops.causal_conv1d_fwd(sets[i][0].transpose(1, 2), sets[i][1], None,
+                                                    True),
+                    len(sets), max(4, steps // len(sets)), warmup)
+    algo = 2 * _bytes(x) + _bytes(w)   # x read, y written, weights
+    Bd, L = 64, 4
+    xt = torch.randn(Bd, 1, D, generator=gen).bfloat16()
+    st = torch.randn(Bd, D, L, generator=gen).bfloat16()
+    per_d = _bytes(xt, st)
+    dsets = rotation(lambda: (xt, st, w), per_d, dev)
+    ms_d = time_graph(lambda i: ops.causal_conv1d_update(dsets[i][0].transpose(1, 2), dsets[i][1],
+                                                         dsets[i][2], None, True),
+                      len(dsets), max(4, steps // len(dsets)), warmup)
+    algo_d = 2 * _bytes(xt) + 2 * _bytes(st) + _bytes(w)   # x, y; state read + written
+    return dict(ms=ms, gbs=algo / ms / 1e6, frac=algo / ms / 1e6 / HBM_PEAK_GBS,
+                ms_d=ms_d, gbs_d=algo_d / ms_d / 1e6, frac_d=algo_d / ms_d / 1e6 / HBM_PEAK_GBS)
 
 
 # Algorithmic FLOPs per chunk-head of each prefill kernel (C = 64, dk = dv = 128,
@@ -370,6 +400,7 @@ def main():
         nrm = bench_norm(ops, dev, args.steps, args.warmup)
         dec = bench_decode(ops, dev, max(20, args.steps // 4), args.warmup)
         var = bench_varlen(ops, dev, max(10, args.steps // 10), 5)
+        cv = bench_conv(ops, dev, args.steps, args.warmup)
         line["secondary"] = {
             "gated_rmsnorm_1141x32x128": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                                  "hbm_frac": round(nrm["frac"], 4)},
@@ -378,6 +409,12 @@ def main():
             "varlen_prefill_8seq_19861tok": {"us": round(var["ms"] * 1e3, 2),
                                   "TFLOP/s": round(var["tflops"], 3),
                                   "tokens": var["tokens"]},
+            "causal_conv1d_silu_1141x8192_k4": {"us": round(cv["ms"] * 1e3, 2),
+                                                "GB/s": round(cv["gbs"], 1),
+                                                "hbm_frac": round(cv["frac"], 4)},
+            "causal_conv1d_update_B64x8192_k4": {"us": round(cv["ms_d"] * 1e3, 2),
+                                                 "GB/s": round(cv["gbs_d"], 1),
+                                                 "hbm_frac": round(cv["frac_d"], 4)},
         }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()

@@ -128,6 +128,35 @@ hipError_t gdn_gated_rmsnorm_forward(const void* x, const void* z, const void* w
                                      int64_t rows, int dv, float eps, int io_dtype, int w_dtype,
                                      hipStream_t stream);
 
+/* Causal depthwise conv1d over time with optional SiLU (no counterpart in the
+ * reference's kernels: the step upstream of q/k/v that transformers runs as
+ * causal_conv1d_fn, models/qwen3_5/modeling_qwen3_5.py:219-240,470-476).
+ * x, y: [B][T][D] of io_dtype (GDN_DTYPE_BF16 or GDN_DTYPE_FP16) with
+ * channels contiguous and the given batch / token strides (elements,
+ * multiples of 8; 16-byte aligned bases); w: [D][K] and bias: [D] (or NULL)
+ * of w_dtype (io_dtype or GDN_DTYPE_FP32).  D a multiple of 8, K in 2..4,
+ * silu 0 or 1.  Tokens before the first are zero.
+ * y = io(act(w_dtype(sum_j w[j] x[t-K+1+j] + bias))), the sum in fp32 with
+ * the taps oldest first and the bias last. */
+hipError_t gdn_causal_conv1d_fwd(const void* x, const void* w, const void* bias, void* y, int B,
+                                 int T, int D, int K, int64_t x_bstride, int64_t x_tstride,
+                                 int64_t y_bstride, int64_t y_tstride, int io_dtype, int w_dtype,
+                                 int silu, hipStream_t stream);
+
+/* Decode-time update of the same conv (causal_conv1d_update,
+ * modeling_qwen3_5.py:199-216,457-463): the window is conv_state's state_len
+ * tokens followed by the T new ones; y gets the last T outputs and conv_state
+ * (updated in place) the window's last state_len tokens.  x, y: [B][D][T]
+ * and conv_state: [B][D][state_len], all io_dtype, with the given strides
+ * (elements; the state's token stride is 1); state_len in K-1..8; dtypes,
+ * K and silu as in gdn_causal_conv1d_fwd. */
+hipError_t gdn_causal_conv1d_update(const void* x, void* conv_state, const void* w,
+                                    const void* bias, void* y, int B, int T, int D, int K,
+                                    int state_len, int64_t x_bstride, int64_t x_tstride,
+                                    int64_t x_dstride, int64_t s_bstride, int64_t s_dstride,
+                                    int64_t y_bstride, int64_t y_tstride, int64_t y_dstride,
+                                    int io_dtype, int w_dtype, int silu, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,8 @@ transformers 5.14.1 ``models/qwen3_5/modeling_qwen3_5.py``:
 * ``chunk_gated_delta_rule`` -> modeling_qwen3_5.py:249-327 (== parity_test.py:35-96)
 * ``recurrent_gated_delta_rule`` -> modeling_qwen3_5.py:331-380
 * ``gated_rmsnorm``          -> modeling_qwen3_5.py:168-184 (Qwen3_5RMSNormGated)
+* ``causal_conv1d``          -> modeling_qwen3_5.py:219-240 (causal_conv1d_fn)
+* ``causal_conv1d_update``   -> modeling_qwen3_5.py:199-216
 * ``gdn_gate``               -> export/patches/orin_text_engine/files/cpp/kernels/
                                 gdnKernels/gdnChunkPrefillSm87.cu:113-125
 * GQA head map               -> kernels/chunk_delta_cuda.h:12-14 (repeat_interleave)
@@ -51,6 +53,8 @@ __all__ = [
     "recurrence_fp64",
     "gated_rmsnorm",
     "unit_lower_inverse",
+    "causal_conv1d",
+    "causal_conv1d_update",
 ]
 
 
@@ -274,3 +278,54 @@ def gated_rmsnorm(x, z, weight, eps=1e-6):
     h = weight * n
     h = h * F.silu(z.to(torch.float32))
     return h.to(in_dtype)
+
+
+def _conv_valid(win, weight, bias, activation, t_out):
+    """Last ``t_out`` outputs of the valid depthwise correlation over ``win``
+    ([B, D, L] already in the weight dtype), with the dtype steps of the
+    transformers functions: the sum in fp32 (taps oldest first, each tap a
+    multiply-add rounded once to fp32, as a fused multiply-add, then the bias
+    added -- the order of torch's CPU convolution, which this reproduces bit
+    for bit), the result rounded to the weight dtype (F.conv1d runs in that
+    dtype), SiLU in fp32 on the rounded value and rounded again.
+    """
+    wd = weight.dtype
+    B, D, L = win.shape
+    K = weight.shape[-1]
+    n = L - K + 1
+    xw = win.to(torch.float64)
+    w64 = weight.to(torch.float64)
+    acc = torch.zeros(B, D, n, dtype=torch.float32)
+    for j in range(K):
+        # fp32 * fp32 is exact in fp64, so one rounding to fp32 per tap
+        acc = (acc.to(torch.float64) + w64[None, :, j:j + 1] * xw[:, :, j:j + n]).to(torch.float32)
+    if bias is not None:
+        acc = acc + bias.to(torch.float32)[None, :, None]
+    out = acc.to(wd)
+    if activation is not None:
+        if activation not in ("silu", "swish"):
+            raise ValueError(f"unsupported activation {activation!r}")
+        out = F.silu(out.to(torch.float32)).to(wd)
+    return out[:, :, n - t_out:]
+
+
+def causal_conv1d(x, weight, bias=None, activation=None):
+    """causal_conv1d_fn (modeling_qwen3_5.py:219-240): depthwise conv over
+    time with K-1 zero tokens before the first, x [B, D, T], weight [D, K],
+    bias [D] or None; returns [B, D, T] in x's dtype."""
+    K = weight.shape[-1]
+    T = x.shape[-1]
+    win = F.pad(x.to(weight.dtype), (K - 1, 0))
+    return _conv_valid(win, weight, bias, activation, T).to(x.dtype)
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
+    """causal_conv1d_update (modeling_qwen3_5.py:199-216) without the in-place
+    write: the window is conv_state [B, D, L] followed by x [B, D, T];
+    returns (y [B, D, T] in x's dtype, the new state = the window's last L
+    tokens in conv_state's dtype)."""
+    L = conv_state.shape[-1]
+    T = x.shape[-1]
+    win = torch.cat([conv_state, x], dim=-1).to(weight.dtype)
+    new_state = win[:, :, -L:].to(conv_state.dtype)
+    return _conv_valid(win, weight, bias, activation, T).to(x.dtype), new_state

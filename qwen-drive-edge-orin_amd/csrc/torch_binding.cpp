@@ -8,8 +8,9 @@
 // the caching allocator on the current stream and calls the C ABI of
 // libgdn_hip.so (include/gdn_hip.h) with raw pointers; no torch types cross
 // that boundary.  New relative to the reference: a trailing keyword
-// `cu_seqlens` (varlen prefill), `recurrent_step` (decode) and
-// `gated_rmsnorm`.
+// `cu_seqlens` (varlen prefill), `recurrent_step` (decode),
+// `gated_rmsnorm` and the causal conv1d ops `causal_conv1d_fwd` /
+// `causal_conv1d_update` that produce q/k/v upstream of the recurrence.
 #include <torch/extension.h>
 
 // ROCm torch reports HIP devices as DeviceType::CUDA; the *MasqueradingAsCUDA
@@ -213,6 +214,87 @@ at::Tensor gated_rmsnorm(at::Tensor x, at::Tensor z, at::Tensor weight, double e
     return y;
 }
 
+int conv_io_dtype(const at::Tensor& x) {
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf,
+                "x must be bf16 or fp16");
+    return x.scalar_type() == at::kBFloat16 ? GDN_DTYPE_BF16 : GDN_DTYPE_FP16;
+}
+
+int conv_w_dtype(const at::Tensor& x, const at::Tensor& w, const std::optional<at::Tensor>& bias) {
+    TORCH_CHECK(w.scalar_type() == x.scalar_type() || w.scalar_type() == at::kFloat,
+                "weight must have the dtype of x or be fp32");
+    TORCH_CHECK(!bias || bias->scalar_type() == w.scalar_type(),
+                "bias must have the dtype of weight");
+    return w.scalar_type() == at::kFloat ? GDN_DTYPE_FP32 : conv_io_dtype(x);
+}
+
+// x: [B, D, T] (a transposed view of a channel-contiguous [B, T, D] buffer is
+// used as is; anything else is first copied into that layout), weight
+// [D, K], bias [D] or None.  Returns y: [B, D, T], a view of a contiguous
+// [B, T, D] buffer (so y.transpose(1, 2) is contiguous).
+at::Tensor causal_conv1d_fwd(const at::Tensor& x, const at::Tensor& weight,
+                             const std::optional<at::Tensor>& bias, bool silu) {
+    TORCH_CHECK(x.is_cuda() && weight.is_cuda() && (!bias || bias->is_cuda()),
+                "all inputs must be CUDA tensors");
+    TORCH_CHECK(x.dim() == 3, "x must be [B, D, T]");
+    const int64_t B = x.size(0), D = x.size(1), T = x.size(2);
+    TORCH_CHECK(weight.dim() == 2 && weight.size(0) == D, "weight must be [D, K]");
+    TORCH_CHECK(!bias || (bias->dim() == 1 && bias->size(0) == D), "bias must be [D]");
+    TORCH_CHECK(D % 8 == 0, "the channel count must be a multiple of 8");
+    const int io = conv_io_dtype(x), wd = conv_w_dtype(x, weight, bias);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    auto xt = x.transpose(1, 2);   // [B, T, D]
+    const bool direct = xt.stride(2) == 1 && (B <= 1 || xt.stride(0) % 8 == 0) &&
+                        (T <= 1 || xt.stride(1) % 8 == 0) &&
+                        reinterpret_cast<uintptr_t>(xt.data_ptr()) % 16 == 0;
+    if (!direct) xt = xt.contiguous();
+    auto wc = weight.contiguous();
+    std::optional<at::Tensor> bc;
+    if (bias) bc = bias->contiguous();
+    auto yt = at::empty({B, T, D}, x.options());
+    check_hip(gdn_causal_conv1d_fwd(xt.data_ptr(), wc.data_ptr(), bc ? bc->data_ptr() : nullptr,
+                                    yt.data_ptr(), (int)B, (int)T, (int)D, (int)wc.size(1),
+                                    B <= 1 ? 0 : xt.stride(0), T <= 1 ? 0 : xt.stride(1),
+                                    yt.stride(0), yt.stride(1), io, wd, silu ? 1 : 0,
+                                    current_stream()),
+              "gdn_causal_conv1d_fwd");
+    return yt.transpose(1, 2);
+}
+
+// x: [B, D, T] (any strides), conv_state: [B, D, L] with unit token stride,
+// updated in place; weight [D, K]; bias [D] or None.  Returns y [B, D, T]
+// laid out like causal_conv1d_fwd's.
+at::Tensor causal_conv1d_update(const at::Tensor& x, at::Tensor conv_state,
+                                const at::Tensor& weight, const std::optional<at::Tensor>& bias,
+                                bool silu) {
+    TORCH_CHECK(x.is_cuda() && conv_state.is_cuda() && weight.is_cuda() &&
+                    (!bias || bias->is_cuda()),
+                "all inputs must be CUDA tensors");
+    TORCH_CHECK(x.dim() == 3, "x must be [B, D, T]");
+    const int64_t B = x.size(0), D = x.size(1), T = x.size(2);
+    TORCH_CHECK(conv_state.dim() == 3 && conv_state.size(0) == B && conv_state.size(1) == D,
+                "conv_state must be [B, D, L]");
+    TORCH_CHECK(conv_state.scalar_type() == x.scalar_type(), "conv_state must have the dtype of x");
+    TORCH_CHECK(conv_state.stride(2) == 1 || conv_state.size(2) == 1,
+                "conv_state must have unit stride along its last dimension");
+    TORCH_CHECK(weight.dim() == 2 && weight.size(0) == D, "weight must be [D, K]");
+    TORCH_CHECK(!bias || (bias->dim() == 1 && bias->size(0) == D), "bias must be [D]");
+    const int io = conv_io_dtype(x), wd = conv_w_dtype(x, weight, bias);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    auto wc = weight.contiguous();
+    std::optional<at::Tensor> bc;
+    if (bias) bc = bias->contiguous();
+    auto y = at::empty({B, T, D}, x.options()).transpose(1, 2);
+    check_hip(gdn_causal_conv1d_update(x.data_ptr(), conv_state.data_ptr(), wc.data_ptr(),
+                                       bc ? bc->data_ptr() : nullptr, y.data_ptr(), (int)B, (int)T,
+                                       (int)D, (int)wc.size(1), (int)conv_state.size(2),
+                                       x.stride(0), x.stride(2), x.stride(1), conv_state.stride(0),
+                                       conv_state.stride(1), y.stride(0), y.stride(2), y.stride(1),
+                                       io, wd, silu ? 1 : 0, current_stream()),
+              "gdn_causal_conv1d_update");
+    return y;
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     using namespace pybind11::literals;
     m.def("chunk_prefill", &chunk_prefill,
@@ -228,4 +310,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "v"_a, "g"_a, "beta"_a, "state"_a);
     m.def("gated_rmsnorm", &gated_rmsnorm, "y = rmsnorm(x) * weight * silu(z)", "x"_a, "z"_a,
           "weight"_a, "eps"_a = 1e-6);
+    m.def("causal_conv1d_fwd", &causal_conv1d_fwd,
+          "causal depthwise conv1d over x [B, D, T] with optional SiLU; returns y [B, D, T]",
+          "x"_a, "weight"_a, "bias"_a = std::nullopt, "silu"_a = false);
+    m.def("causal_conv1d_update", &causal_conv1d_update,
+          "decode-time causal conv1d; conv_state [B, D, L] updated in place; returns y", "x"_a,
+          "conv_state"_a, "weight"_a, "bias"_a = std::nullopt, "silu"_a = false);
 }

@@ -12,6 +12,9 @@ The compiled pieces live next to this file:
   chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
   recurrent_step(q, k, v, g, beta, state) -> o          (state updated in place)
   gated_rmsnorm(x, z, weight, eps=1e-6) -> y
+  causal_conv1d_fwd(x, weight, bias=None, silu=False) -> y      x, y [B, D, T]
+  causal_conv1d_update(x, conv_state, weight, bias=None, silu=False) -> y
+                                                  (conv_state updated in place)
 
 There is no fallback: if the extension is not built, ``load()`` raises.
 Build with ``python qwen-drive-edge-orin_amd/build.py``.
@@ -60,3 +63,11 @@ def recurrent_step(q, k, v, g, beta, state):
 
 def gated_rmsnorm(x, z, weight, eps=1e-6):
     return load().gated_rmsnorm(x, z, weight, eps)
+
+
+def causal_conv1d_fwd(x, weight, bias=None, silu=False):
+    return load().causal_conv1d_fwd(x, weight, bias, silu)
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, silu=False):
+    return load().causal_conv1d_update(x, conv_state, weight, bias, silu)

@@ -43,6 +43,10 @@ _PROTOS = {
                                       [vp, c_size_t, hipStream_t, c_int]),
     "gdn_gated_rmsnorm_forward": (hipError_t, [vp, vp, vp, vp, c_int64, c_int, c_float, c_int,
                                                c_int, hipStream_t]),
+    "gdn_causal_conv1d_fwd": (hipError_t, [vp, vp, vp, vp] + [c_int] * 4 + [c_int64] * 4 +
+                              [c_int] * 3 + [hipStream_t]),
+    "gdn_causal_conv1d_update": (hipError_t, [vp, vp, vp, vp, vp] + [c_int] * 5 + [c_int64] * 8 +
+                                 [c_int] * 3 + [hipStream_t]),
 }
 
 

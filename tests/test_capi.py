@@ -124,11 +124,50 @@ def test_decode_and_norm_reject_on_host(lib):
     assert nrm(None, 1, 1, 1, 10, 128, 1e-6, capi.DTYPE_BF16, capi.DTYPE_BF16, None) == INVALID
 
 
+def test_conv_reject_on_host(lib):
+    fwd = lib.gdn_causal_conv1d_fwd
+    bf, fp32 = capi.DTYPE_BF16, capi.DTYPE_FP32
+    # x, w, bias, y, B, T, D, K, strides (x b/t, y b/t), io, w dtype, silu, stream
+    ok = [16, 16, None, 16, 1, 8, 64, 4, 0, 64, 0, 64, bf, bf, 1, None]
+
+    def f(**over):
+        a = list(ok)
+        for i, v in over.items():
+            a[int(i[1:])] = v
+        return fwd(*a)
+
+    assert f(a7=5) == INVALID and f(a7=1) == INVALID          # K outside 2..4
+    assert f(a6=60) == INVALID                                # D % 8
+    assert f(a12=fp32, a13=fp32) == INVALID                   # fp32 activations
+    assert f(a13=capi.DTYPE_FP16) == INVALID                  # mixed 16-bit dtypes
+    assert f(a14=2) == INVALID                                # silu flag
+    assert f(a9=68) == INVALID                                # token stride not 8-aligned
+    assert f(a0=8) == INVALID                                 # x not 16-byte aligned
+    assert f(a0=None) == INVALID and f(a1=None) == INVALID and f(a3=None) == INVALID
+    assert f(a4=0) == 0 and f(a5=0) == 0                      # empty: nothing to launch
+    upd = lib.gdn_causal_conv1d_update
+    # x, state, w, bias, y, B, T, D, K, L, x b/t/d, s b/d, y b/t/d, io, w dtype, silu, stream
+    uok = [16, 16, 16, None, 16, 1, 1, 64, 4, 4, 64, 64, 1, 256, 4, 64, 64, 1, bf, fp32, 1, None]
+
+    def u(**over):
+        a = list(uok)
+        for i, v in over.items():
+            a[int(i[1:])] = v
+        return upd(*a)
+
+    assert u(a9=2) == INVALID and u(a9=9) == INVALID          # state_len outside K-1..8
+    assert u(a8=5) == INVALID
+    assert u(a1=None) == INVALID and u(a2=None) == INVALID
+    assert u(a18=fp32) == INVALID
+    assert u(a6=0) == 0
+
+
 def test_torch_extension_loads_and_checks_device():
     import torch
 
     ops = gdn_hip.load()
-    for name in ("chunk_prefill", "chunk_prefill_debug", "recurrent_step", "gated_rmsnorm"):
+    for name in ("chunk_prefill", "chunk_prefill_debug", "recurrent_step", "gated_rmsnorm",
+                 "causal_conv1d_fwd", "causal_conv1d_update"):
         assert hasattr(ops, name)
     q = torch.zeros(1, 64, 2, 128, dtype=torch.bfloat16)
     v = torch.zeros(1, 64, 4, 128, dtype=torch.bfloat16)
@@ -137,3 +176,6 @@ def test_torch_extension_loads_and_checks_device():
         ops.chunk_prefill(q, q, v, g, g, None)
     with pytest.raises(RuntimeError, match="CUDA"):
         ops.gated_rmsnorm(v, v, torch.ones(128, dtype=torch.bfloat16), 1e-6)
+    x = torch.zeros(1, 64, 8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        ops.causal_conv1d_fwd(x, torch.zeros(64, 4, dtype=torch.bfloat16), None, True)

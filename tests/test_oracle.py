@@ -268,3 +268,148 @@ def test_matches_transformers_chunk_and_recurrent():
                                                     output_final_state=True)
     assert _err(o_r, o_rt) < 1e-5 and _err(S_r, S_rt) < 1e-5
     assert _err(orc.l2norm(v), m.l2norm(v, dim=-1, eps=1e-6)) == 0.0
+
+
+# ------------------------------------------------------- causal conv1d (f3)
+
+
+def _conv_brute(x, w, bias, silu):
+    """Depthwise causal correlation by explicit loops in Python floats
+    (fp64), x [B, D, T], w [D, K]; no dtype steps (fp32 inputs)."""
+    B, D, T = x.shape
+    K = w.shape[1]
+    y = torch.zeros(B, D, T, dtype=F64)
+    for b in range(B):
+        for d in range(D):
+            for t in range(T):
+                s = 0.0 if bias is None else float(bias[d])
+                for j in range(K):
+                    tt = t - (K - 1) + j
+                    if tt >= 0:
+                        s += float(w[d, j]) * float(x[b, d, tt])
+                y[b, d, t] = s / (1.0 + math.exp(-s)) if silu else s
+    return y
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("silu", [False, True])
+def test_conv_matches_brute_force(K, silu):
+    gen = torch.Generator().manual_seed(30 + K)
+    x = torch.randn(2, 5, 9, generator=gen)
+    w = torch.randn(5, K, generator=gen)
+    bias = torch.randn(5, generator=gen)
+    for bb in (None, bias):
+        y = orc.causal_conv1d(x, w, bb, "silu" if silu else None)
+        assert _err(y, _conv_brute(x, w, bb, silu)) < 1e-5
+
+
+def test_conv_closed_forms():
+    # a unit impulse at token 3 reproduces the taps in reverse time order
+    x = torch.zeros(1, 2, 8)
+    x[0, :, 3] = 1.0
+    w = torch.tensor([[1.0, 2.0, 3.0, 4.0], [-1.0, 0.5, 0.25, 8.0]])
+    y = orc.causal_conv1d(x, w)
+    assert torch.equal(y[0, :, 3:7], w.flip(-1))
+    assert torch.equal(y[0, :, :3], torch.zeros(2, 3)) and torch.equal(y[0, :, 7], torch.zeros(2))
+    # the first output only sees the newest tap (causality, zero history)
+    x = torch.randn(1, 3, 5, generator=torch.Generator().manual_seed(3))
+    w = torch.randn(3, 4, generator=torch.Generator().manual_seed(4))
+    assert _err(orc.causal_conv1d(x, w)[0, :, 0], w[:, 3] * x[0, :, 0]) < 1e-7
+
+
+def _conv_inputs(seed, io, wd, D=64, T=200, K=4, B=2):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, T, D, generator=gen).to(io).transpose(1, 2)
+    w = (0.5 * torch.randn(D, K, generator=gen)).to(wd)
+    bias = (0.1 * torch.randn(D, generator=gen)).to(wd)
+    return x, w, bias
+
+
+def _tf_conv():
+    m = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    # the undecorated torch functions (the decorator may route to a package)
+    return (getattr(m.causal_conv1d_fn, "__wrapped__", m.causal_conv1d_fn),
+            getattr(m.causal_conv1d_update, "__wrapped__", m.causal_conv1d_update))
+
+
+@pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_conv_matches_transformers_bitwise(io, K):
+    fn, _ = _tf_conv()
+    x, w, bias = _conv_inputs(40 + K, io, io, K=K)
+    for bb in (None, bias):
+        for act in (None, "silu"):
+            assert torch.equal(orc.causal_conv1d(x, w, bb, act), fn(x, w, bb, act))
+
+
+def test_conv_fp32_weights_match_transformers_within_an_ulp():
+    # fp32 convolution: torch's CPU kernel sums in another order, so the
+    # final rounding to bf16 may differ by one unit in rare elements
+    fn, _ = _tf_conv()
+    x, w, bias = _conv_inputs(50, torch.bfloat16, torch.float32, D=256, T=300)
+    a = orc.causal_conv1d(x, w, bias, "silu").float()
+    r = fn(x, w, bias, "silu").float()
+    ulp = torch.maximum(a.abs(), r.abs()).clamp_min(1e-30) * 2.0 ** -7
+    assert ((a - r).abs() <= ulp).all()
+    assert (a != r).float().mean().item() < 1e-3
+
+
+@pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [1, 3])
+def test_conv_update_matches_transformers(io, T):
+    _, up = _tf_conv()
+    gen = torch.Generator().manual_seed(60 + T)
+    x = torch.randn(2, 64, T, generator=gen).to(io)
+    st = torch.randn(2, 64, 4, generator=gen).to(io)
+    w = (0.5 * torch.randn(64, 4, generator=gen)).to(io)
+    bias = (0.1 * torch.randn(64, generator=gen)).to(io)
+    st_t = st.clone()
+    r = up(x, st_t, w, bias, "silu")
+    y, ns = orc.causal_conv1d_update(x, st, w, bias, "silu")
+    assert torch.equal(y, r) and torch.equal(ns, st_t)
+
+
+@pytest.mark.parametrize("L", [3, 4, 6])
+def test_conv_prefill_then_updates_equals_one_pass(L):
+    # resuming from the carried state reproduces the one-pass outputs exactly
+    x, w, bias = _conv_inputs(70, torch.bfloat16, torch.bfloat16, D=32, T=40)
+    full = orc.causal_conv1d(x, w, bias, "silu")
+    split = 29
+    state = F.pad(x[:, :, :split], (L, 0))[:, :, -L:]   # zeros before the first token
+    outs = [orc.causal_conv1d(x[:, :, :split], w, bias, "silu")]
+    for t0, n in ((29, 1), (30, 3), (33, 1), (34, 6)):
+        y, state = orc.causal_conv1d_update(x[:, :, t0:t0 + n], state, w, bias, "silu")
+        outs.append(y)
+    assert torch.equal(torch.cat(outs, dim=-1), full)
+    assert torch.equal(state, x[:, :, -L:])
+
+
+def _mutant_conv(x, w, bias, act, mutation):
+    """The conv oracle's formula with one planted mistake (test only)."""
+    K = w.shape[-1]
+    T = x.shape[-1]
+    xp = F.pad(x.to(w.dtype).float(), (K - 1, 0))
+    wf = w.float().flip(-1) if mutation == "reversed_taps" else w.float()
+    off = 1 if mutation == "shift" else 0
+    xp = F.pad(xp, (off, 0))
+    acc = sum(wf[None, :, j:j + 1] * xp[:, :, j:j + T] for j in range(K))
+    if bias is not None:
+        acc = acc + bias.float()[None, :, None]
+    out = acc if mutation == "no_weight_rounding" else acc.to(w.dtype).float()
+    if act is not None:
+        out = F.silu(out)
+    return out.to(x.dtype)
+
+
+@pytest.mark.parametrize("mutation", ["reversed_taps", "shift", "no_weight_rounding"])
+def test_conv_pins_detect_planted_mistakes(mutation):
+    # fp32: the brute-force loop pin
+    gen = torch.Generator().manual_seed(80)
+    x = torch.randn(1, 6, 12, generator=gen)
+    w = torch.randn(6, 4, generator=gen)
+    brute_err = _err(_mutant_conv(x, w, None, "silu", mutation), _conv_brute(x, w, None, True))
+    # bf16: the bitwise transformers pin
+    fn, _ = _tf_conv()
+    xb, wb, bb = _conv_inputs(81, torch.bfloat16, torch.bfloat16)
+    tf_equal = torch.equal(_mutant_conv(xb, wb, bb, "silu", mutation), fn(xb, wb, bb, "silu"))
+    assert brute_err > 1e-3 or not tf_equal, f"pins missed planted mistake {mutation}"
