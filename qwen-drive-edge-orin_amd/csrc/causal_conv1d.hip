@@ -12,19 +12,21 @@
 //
 // Layout: x and y are [B][T][D] with channels contiguous (transformers hands
 // a transposed view of exactly that), so a lane moves 16 bytes = 8 channels
-// of one token.  A thread owns 8 channels and kConvTT consecutive tokens and
-// keeps the K-token window in registers; neighbouring token tiles overlap by
-// K-1 rows (L2 hits).  Purely HBM-bound: x read once, y written once.
+// of one token.  A thread owns 8 channels and a run of consecutive tokens and
+// keeps the K-token window in registers; neighbouring runs overlap by K-1
+// rows (L2 hits).  HBM-bound: x read once, y written once.
 #include "gdn_common.h"
 #include "gdn_hip.h"
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace gdn {
 namespace {
 
 constexpr int kConvThreads = 256;
-constexpr int kConvTT = 8;          // tokens per thread
+constexpr int kConvMaxRun = 12;     // longest token run of one work-group
 constexpr int kConvMaxState = 8;    // longest carried state of the update
 
 // element loads / stores by dtype code (0 bf16, 1 fp16, 2 fp32)
@@ -44,47 +46,120 @@ __device__ inline float cv_load(uint32_t bits16) {
 template <int IO>
 __device__ inline uint32_t cv_store(float f) {
     if constexpr (IO == 0) return f32_to_bf16_bits(f);
+    // the fp32 value must exist before it is rounded: fused into the
+    // producing multiply-add (v_fma_mixlo_f16) the sum is rounded to fp16
+    // once instead of to fp32 first, which differs in rare ties
+    asm("" : "+v"(f));
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// 16-bit values of a packed pair (element 0 in the low half) as fp32
 template <int IO>
-__device__ inline void unpack8(u32x4 r, float (&f)[8]) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        f[2 * p] = cv_load<IO>(r[p] & 0xffffu);
-        f[2 * p + 1] = cv_load<IO>(r[p] >> 16);
+__device__ inline float lo16(uint32_t u) {
+    if constexpr (IO == 0) return __uint_as_float(u << 16);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
+}
+
+template <int IO>
+__device__ inline float hi16(uint32_t u) {
+    if constexpr (IO == 0) return __uint_as_float(u & 0xffff0000u);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+}
+
+// two fp32 values rounded to nearest-even 16-bit and packed (a low)
+template <int IO>
+__device__ inline uint32_t pack2(float a, float b) {
+    if constexpr (IO == 0) {
+        // one v_cvt_pk_bf16_f32 (written out: from the vector form the
+        // compiler emits a conversion per element plus masking)
+        uint32_t u;
+        asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
+        return u;
+    } else {
+        return cv_store<1>(a) | (cv_store<1>(b) << 16);
     }
 }
 
-// act(round_w(acc)) rounded to the I/O dtype.  With fp32 weights the conv
-// output is already fp32 and only the final rounding remains.
-template <int IO, int WT>
-__device__ inline uint32_t finish(float acc, int silu) {
+// SiLU r / (1 + e^-r) in fp32 from the hardware base-2 exponential and
+// reciprocal (each within about an ulp).  Far below zero (r < -87) the
+// reciprocal underflows to 0 and the result is -0, where exact arithmetic
+// gives |y| < 1e-36.
+__device__ inline float silu_f32(float r) {
+    const float e = __builtin_amdgcn_exp2f(r * -1.44269504088896341f);
+    return r * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// one output: the fp32 sum rounded to the weight dtype (unless fp32), SiLU,
+// rounded to the I/O dtype (16-bit pattern)
+template <int IO, int WT, bool SILU>
+__device__ inline uint32_t finish1(float acc) {
     float r = (WT == 2) ? acc : cv_load<WT>(cv_store<WT>(acc));
-    if (silu) r = r / (1.0f + expf(-r));
+    if constexpr (SILU) r = silu_f32(r);
     return cv_store<IO>(r);
 }
 
-template <int IO, int WT, int K>
+// the same for one token's 8 channels, packed in pairs
+template <int IO, int WT, bool SILU>
+__device__ inline u32x4 finish8(const float (&acc)[8]) {
+    u32x4 out;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        float a = acc[2 * p], b = acc[2 * p + 1];
+        if constexpr (WT != 2) {
+            const uint32_t u = pack2<WT>(a, b);
+            if constexpr (!SILU && WT == IO) {
+                out[p] = u;
+                continue;
+            }
+            a = lo16<WT>(u);
+            b = hi16<WT>(u);
+        }
+        if constexpr (SILU) {
+            a = silu_f32(a);
+            b = silu_f32(b);
+        }
+        out[p] = pack2<IO>(a, b);
+    }
+    return out;
+}
+
+// Work units: (batch, token run, channel tile of 2048) with the channel tile
+// fastest.  The launcher sizes the runs (at most kConvMaxRun tokens, equal
+// lengths but the last) so the grid holds about two waves per SIMD: every
+// SIMD then gets the same number of equal waves, where fixed short tiles
+// leave some SIMDs one wave more than others.  Work-groups are dealt
+// round-robin to the 8 XCDs (each with its own L2); remapping the
+// work-group id gives every XCD one contiguous range of units, so the K-1
+// halo rows a run shares with the previous run are read from the same L2.
+__device__ inline int xcd_unit(int id, int n) {
+    const int q = n / 8, r = n % 8, xcd = id % 8;
+    return xcd * q + min(xcd, r) + id / 8;
+}
+
+template <int IO, int WT, int K, bool SILU, bool BIAS>
 __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const void* __restrict__ bias,
     uint16_t* __restrict__ y, int T, int D, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
-    int silu) {
-    const int g8 = blockIdx.x * kConvThreads + threadIdx.x;   // 8-channel group
-    if (g8 * 8 >= D) return;
-    const int t0 = blockIdx.y * kConvTT;
-    const int b = blockIdx.z;
-    const int d0 = g8 * 8;
+    int n_ctiles, int n_runs, int run) {
+    const int unit = xcd_unit(blockIdx.x, gridDim.x);
+    const int ct = unit % n_ctiles;
+    const int rest = unit / n_ctiles;
+    const int t0 = (rest % n_runs) * run;
+    const int b = rest / n_runs;
+    const int d0 = (ct * kConvThreads + threadIdx.x) * 8;
+    if (d0 >= D) return;
+    const int len = min(run, T - t0);   // >= 1: the launcher makes n_runs = ceil(T / run)
     const uint16_t* xb = x + (size_t)b * xbs + d0;
     uint16_t* yb = y + (size_t)b * ybs + d0;
-    // all loads first: rows t0-K+1 .. t0+kConvTT-1 (rows before 0 are zero,
-    // rows past T-1 re-read row T-1 and are never stored)
-    u32x4 raw[kConvTT + K - 1];
+    // all loads first: rows t0-K+1 .. t0+len-1; rows before 0 are zero, the
+    // slots past the run re-read its last row (a cache hit) and stay unused
+    constexpr int kRows = kConvMaxRun + K - 1;
+    u32x4 raw[kRows];
 #pragma unroll
-    for (int i = 0; i < kConvTT + K - 1; ++i) {
+    for (int i = 0; i < kRows; ++i) {
         const int t = t0 - (K - 1) + i;
-        const int tc = min(max(t, 0), T - 1);
-        raw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + (size_t)tc * xts));
+        const int tc = min(max(t, 0), t0 + len - 1);
+        raw[i] = *reinterpret_cast<const u32x4*>(xb + (size_t)tc * xts);   // cached: halo rows
         if (t < 0) raw[i] = u32x4{0u, 0u, 0u, 0u};
     }
     float wf[8][K], bf[8];
@@ -92,28 +167,45 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
     for (int e = 0; e < 8; ++e) {
 #pragma unroll
         for (int j = 0; j < K; ++j) wf[e][j] = ld_elem<WT>(w, (size_t)(d0 + e) * K + j);
-        bf[e] = bias ? ld_elem<WT>(bias, d0 + e) : 0.f;
+        if constexpr (BIAS) bf[e] = ld_elem<WT>(bias, d0 + e);
+    }
+    // sliding window of K unpacked rows: win[j] = row i + j
+    float win[K][8];
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            win[j][2 * p] = lo16<IO>(raw[j][p]);
+            win[j][2 * p + 1] = hi16<IO>(raw[j][p]);
+        }
     }
 #pragma unroll
-    for (int i = 0; i < kConvTT; ++i) {
-        const int t = t0 + i;
-        float acc[8];
+    for (int i = 0; i < kConvMaxRun; ++i) {
+        if (i < len) {   // uniform over the work-group
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+            for (int p = 0; p < 4; ++p) {
+                win[K - 1][2 * p] = lo16<IO>(raw[i + K - 1][p]);
+                win[K - 1][2 * p + 1] = hi16<IO>(raw[i + K - 1][p]);
+            }
+            float acc[8];
 #pragma unroll
-        for (int j = 0; j < K; ++j) {
-            float xf[8];
-            unpack8<IO>(raw[i + j], xf);
+            for (int e = 0; e < 8; ++e) {
+                // +0 start: an all-zero window gives +0, as a sum from zero
+                float a = fmaf(wf[e][0], win[0][e], 0.0f);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = fmaf(wf[e][j], xf[e], acc[e]);
+                for (int j = 1; j < K; ++j) a = fmaf(wf[e][j], win[j][e], a);
+                if constexpr (BIAS) a += bf[e];
+                acc[e] = a;
+            }
+            const u32x4 out = finish8<IO, WT, SILU>(acc);
+            __builtin_nontemporal_store(out,
+                                        reinterpret_cast<u32x4*>(yb + (size_t)(t0 + i) * yts));
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += bf[e];
-        u32x4 out;
+        for (int j = 0; j < K - 1; ++j) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-            out[p] = finish<IO, WT>(acc[2 * p], silu) | (finish<IO, WT>(acc[2 * p + 1], silu) << 16);
-        if (t < T) __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(yb + (size_t)t * yts));
+            for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
+        }
     }
 }
 
@@ -123,26 +215,38 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
 // the window, and the state becomes the window's last state_len tokens
 // (modeling_qwen3_5.py:200-216).  The window is read into registers before
 // the state is rewritten, since the two overlap whenever T < state_len.
-template <int IO, int WT, int K>
+template <int IO, int WT, int K, bool SILU>
 __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update_kernel(
     const uint16_t* __restrict__ x, uint16_t* __restrict__ state, const void* __restrict__ w,
     const void* __restrict__ bias, uint16_t* __restrict__ y, int B, int T, int D, int state_len,
     int64_t xbs, int64_t xts, int64_t xds, int64_t sbs, int64_t sds, int64_t ybs, int64_t yts,
-    int64_t yds, int silu) {
+    int64_t yds) {
     const int64_t gid = (int64_t)blockIdx.x * kConvThreads + threadIdx.x;
     if (gid >= (int64_t)B * D) return;
     const int b = (int)(gid / D), d = (int)(gid - (int64_t)b * D);
     float wf[K];
 #pragma unroll
     for (int j = 0; j < K; ++j) wf[j] = ld_elem<WT>(w, (size_t)d * K + j);
-    const float bv = bias ? ld_elem<WT>(bias, d) : 0.f;
+    const float bv = bias ? ld_elem<WT>(bias, d) : 0.f;   // added only with a bias
     uint16_t* st = state + (size_t)b * sbs + (size_t)d * sds;
     const uint16_t* xs = x + (size_t)b * xbs + (size_t)d * xds;
     uint16_t* ys = y + (size_t)b * ybs + (size_t)d * yds;
-    // the old state, then a rolling K-1 history of window values
+    // the old state (one 8-byte access for the common 4-token row), then a
+    // rolling K-1 history of window values
+    const bool row4 = state_len == 4 && sds == 4 && (reinterpret_cast<uintptr_t>(st) & 7) == 0;
     uint16_t old[kConvMaxState];
+    if (row4) {
+        const uint2 u = *reinterpret_cast<const uint2*>(st);
+        old[0] = (uint16_t)u.x;
+        old[1] = (uint16_t)(u.x >> 16);
+        old[2] = (uint16_t)u.y;
+        old[3] = (uint16_t)(u.y >> 16);
 #pragma unroll
-    for (int p = 0; p < kConvMaxState; ++p) old[p] = p < state_len ? st[p] : (uint16_t)0;
+        for (int p = 4; p < kConvMaxState; ++p) old[p] = 0;
+    } else {
+#pragma unroll
+        for (int p = 0; p < kConvMaxState; ++p) old[p] = p < state_len ? st[p] : (uint16_t)0;
+    }
     // hist[K-1] is the newest window value; state_len >= K-1, so the K-1
     // newest state values seed the rest
     float hist[K];
@@ -157,43 +261,71 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update_kernel(
     for (int i = 0; i < T; ++i) {
         const uint16_t xr = xs[(size_t)i * xts];
         hist[K - 1] = cv_load<IO>(xr);
-        float acc = 0.f;
+        float acc = fmaf(wf[0], hist[0], 0.0f);
 #pragma unroll
-        for (int j = 0; j < K; ++j) acc = fmaf(wf[j], hist[j], acc);
-        acc += bv;
-        ys[(size_t)i * yts] = (uint16_t)finish<IO, WT>(acc, silu);
+        for (int j = 1; j < K; ++j) acc = fmaf(wf[j], hist[j], acc);
+        if (bias) acc += bv;
+        ys[(size_t)i * yts] = (uint16_t)finish1<IO, WT, SILU>(acc);
 #pragma unroll
         for (int j = 0; j < K - 1; ++j) hist[j] = hist[j + 1];
     }
     // new state: the window's last state_len tokens.  Entry p is window index
     // q = (L - state_len) + p = T + p (L = state_len + T): an old state value
     // while q < state_len, else new token q - state_len.
-    for (int p = 0; p < state_len; ++p) {
-        const int q = T + p;
-        uint16_t v;
-        if (q < state_len) {
-            v = 0;
+    uint16_t ns[kConvMaxState];
 #pragma unroll
-            for (int r = 0; r < kConvMaxState; ++r) v = (r == q) ? old[r] : v;
-        } else {
-            v = xs[(size_t)(q - state_len) * xts];
+    for (int p = 0; p < kConvMaxState; ++p) {
+        const int q = T + p;
+        uint16_t v = 0;
+        if (p < state_len) {
+            if (q < state_len) {
+#pragma unroll
+                for (int r = 0; r < kConvMaxState; ++r) v = (r == q) ? old[r] : v;
+            } else {
+                v = xs[(size_t)(q - state_len) * xts];
+            }
         }
-        st[p] = v;
+        ns[p] = v;
+    }
+    if (row4) {
+        uint2 u;
+        u.x = (uint32_t)ns[0] | ((uint32_t)ns[1] << 16);
+        u.y = (uint32_t)ns[2] | ((uint32_t)ns[3] << 16);
+        *reinterpret_cast<uint2*>(st) = u;
+    } else {
+#pragma unroll
+        for (int p = 0; p < kConvMaxState; ++p)
+            if (p < state_len) st[p] = ns[p];
     }
 }
 
-template <int IO, int WT>
+template <int IO, int WT, bool SILU, bool BIAS>
 hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, int B, int T, int D,
-                      int K, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts, int silu,
+                      int K, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
                       hipStream_t stream) {
-    const dim3 grid((unsigned)((D / 8 + kConvThreads - 1) / kConvThreads),
-                    (unsigned)((T + kConvTT - 1) / kConvTT), (unsigned)B);
+    const int n_ctiles = (D / 8 + kConvThreads - 1) / kConvThreads;
+    // about two waves per SIMD (2 work-groups of 4 waves per CU), runs of
+    // equal length up to kConvMaxRun tokens
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t per_row = (int64_t)B * n_ctiles;
+    int64_t n_runs = (2LL * cus + per_row / 2) / per_row;
+    n_runs = std::max<int64_t>(1, std::min<int64_t>(n_runs, T));
+    int run = (int)((T + n_runs - 1) / n_runs);
+    run = std::min(run, kConvMaxRun);
+    n_runs = (T + run - 1) / run;
+    const int64_t units = per_row * n_runs;
+    if (units > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)units);
     auto xp = static_cast<const uint16_t*>(x);
     auto yp = static_cast<uint16_t*>(y);
-#define GDN_CONV_FWD(KK)                                                                        \
-    case KK:                                                                                    \
-        hipLaunchKernelGGL((causal_conv1d_fwd_kernel<IO, WT, KK>), grid, dim3(kConvThreads), 0, \
-                           stream, xp, w, bias, yp, T, D, xbs, xts, ybs, yts, silu);            \
+#define GDN_CONV_FWD(KK)                                                                       \
+    case KK:                                                                                   \
+        hipLaunchKernelGGL((causal_conv1d_fwd_kernel<IO, WT, KK, SILU, BIAS>), grid,          \
+                           dim3(kConvThreads), 0, stream, xp, w, bias, yp, T, D, xbs, xts, ybs, \
+                           yts, n_ctiles, (int)n_runs, run);                                   \
         break;
     switch (K) {
         GDN_CONV_FWD(2)
@@ -204,6 +336,17 @@ hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, i
     }
 #undef GDN_CONV_FWD
     return hipGetLastError();
+}
+
+template <int IO, int WT>
+hipError_t launch_fwd_any(const void* x, const void* w, const void* bias, void* y, int B, int T,
+                          int D, int K, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
+                          int silu, hipStream_t stream) {
+#define GDN_FWD_CALL(S, BI) \
+    launch_fwd<IO, WT, S, BI>(x, w, bias, y, B, T, D, K, xbs, xts, ybs, yts, stream)
+    if (silu) return bias ? GDN_FWD_CALL(true, true) : GDN_FWD_CALL(true, false);
+    return bias ? GDN_FWD_CALL(false, true) : GDN_FWD_CALL(false, false);
+#undef GDN_FWD_CALL
 }
 
 template <int IO, int WT>
@@ -218,9 +361,14 @@ hipError_t launch_update(const void* x, void* state, const void* w, const void* 
     auto yp = static_cast<uint16_t*>(y);
 #define GDN_CONV_UPD(KK)                                                                        \
     case KK:                                                                                    \
-        hipLaunchKernelGGL((causal_conv1d_update_kernel<IO, WT, KK>), grid, dim3(kConvThreads), \
-                           0, stream, xp, sp, w, bias, yp, B, T, D, state_len, xbs, xts, xds,   \
-                           sbs, sds, ybs, yts, yds, silu);                                      \
+        if (silu)                                                                               \
+            hipLaunchKernelGGL((causal_conv1d_update_kernel<IO, WT, KK, true>), grid,          \
+                               dim3(kConvThreads), 0, stream, xp, sp, w, bias, yp, B, T, D,     \
+                               state_len, xbs, xts, xds, sbs, sds, ybs, yts, yds);              \
+        else                                                                                    \
+            hipLaunchKernelGGL((causal_conv1d_update_kernel<IO, WT, KK, false>), grid,         \
+                               dim3(kConvThreads), 0, stream, xp, sp, w, bias, yp, B, T, D,     \
+                               state_len, xbs, xts, xds, sbs, sds, ybs, yts, yds);              \
         break;
     switch (K) {
         GDN_CONV_UPD(2)
@@ -250,7 +398,6 @@ extern "C" hipError_t gdn_causal_conv1d_fwd(const void* x, const void* w, const 
                                             int w_dtype, int silu, hipStream_t stream) {
     if (B < 0 || T < 0 || D <= 0 || D % 8 != 0 || K < 2 || K > 4) return hipErrorInvalidValue;
     if (!conv_dtypes_ok(io_dtype, w_dtype) || (silu != 0 && silu != 1)) return hipErrorInvalidValue;
-    if (B > 65535 || (int64_t)T > 65535LL * kConvTT) return hipErrorInvalidValue;   // grid y, z
     if (B == 0 || T == 0) return hipSuccess;
     if (!x || !w || !y) return hipErrorInvalidValue;
     // 16-byte lane accesses: every row start must stay 16-byte aligned
@@ -259,8 +406,8 @@ extern "C" hipError_t gdn_causal_conv1d_fwd(const void* x, const void* w, const 
         return hipErrorInvalidValue;
     const bool bf = io_dtype == GDN_DTYPE_BF16, w32 = w_dtype == GDN_DTYPE_FP32;
 #define GDN_FWD_ARGS x, w, bias, y, B, T, D, K, x_bstride, x_tstride, y_bstride, y_tstride, silu, stream
-    if (bf) return w32 ? launch_fwd<0, 2>(GDN_FWD_ARGS) : launch_fwd<0, 0>(GDN_FWD_ARGS);
-    return w32 ? launch_fwd<1, 2>(GDN_FWD_ARGS) : launch_fwd<1, 1>(GDN_FWD_ARGS);
+    if (bf) return w32 ? launch_fwd_any<0, 2>(GDN_FWD_ARGS) : launch_fwd_any<0, 0>(GDN_FWD_ARGS);
+    return w32 ? launch_fwd_any<1, 2>(GDN_FWD_ARGS) : launch_fwd_any<1, 1>(GDN_FWD_ARGS);
 #undef GDN_FWD_ARGS
 }
 

@@ -32,6 +32,10 @@ __device__ inline float load_elem(uint32_t bits) {
 template <int IO>
 __device__ inline uint32_t store_elem(float f) {
     if (IO == 0) return f32_to_bf16_bits(f);
+    // the fp32 value must exist before it is rounded: fused into the
+    // producing multiply(-add) (v_fma_mixlo_f16) the product is rounded to
+    // fp16 once instead of to fp32 first, which differs in rare ties
+    asm("" : "+v"(f));
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
