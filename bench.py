@@ -9,7 +9,7 @@ resident in HBM before timing starts; successive steps rotate through enough
 input copies (> 256 MB) that the Infinity Cache cannot serve them, so the
 timed number is the cold one.  The warm (same inputs every step) number and
 the secondary workloads (gated RMSNorm, decode step, varlen prefill, causal
-conv1d prefill and decode update) are
+conv1d prefill and decode update, the fused raw-input prefill) are
 reported in the same JSON line.
 
 Prints ONE JSON line.  `value` is TFLOP/s under the fixed dense FLOP
@@ -144,6 +144,34 @@ def bench_norm(ops, dev, steps, warmup):
                     len(sets), max(4, steps // len(sets)), warmup)
     algo = per + _bytes(x)
     return dict(ms=ms, gbs=algo / ms / 1e6, frac=algo / ms / 1e6 / HBM_PEAK_GBS, bytes=algo)
+
+
+def bench_fused(ops, dev, steps, warmup):
+    """The fused prefill on the plugin's raw fp16 inputs (q/k L2 norm, gate
+    math, conversions and the in-place state inside the two kernels) at
+    T=1141 HV=32 HK=16, against the same step done as the reference adapter
+    does it: separate normalisation, conversion and gate passes (here torch
+    ops on the GPU), the prefill, the o conversion and a state copy."""
+    import torch
+    import gdn_cases as gc
+    from oracle import gdn_oracle as orc
+
+    q, k, v, a, b, A_log, dt_bias, s0 = gc.fused_inputs(20, B=1, T=1141, HK=16, HV=32)
+    per = _bytes(q, k, v, a, b, s0)
+    sets = rotation(lambda: (q, k, v, a, b, A_log, dt_bias, s0), per, dev)
+    ms_f = time_calls(lambda i: ops.chunk_prefill_fused(*sets[i]), len(sets), steps, warmup)
+
+    def chain(i):
+        qq, kk, vv, aa, bb, Al, dt, st = sets[i]
+        qn = orc.l2norm(qq.float()).to(torch.bfloat16)
+        kn = orc.l2norm(kk.float()).to(torch.bfloat16)
+        g, beta = orc.gdn_gate(aa, bb, Al, dt)
+        o, sf = ops.chunk_prefill(qn, kn, vv.to(torch.bfloat16), g, beta, st)
+        o.to(torch.float16)
+        st.copy_(sf)
+
+    ms_c = time_calls(chain, len(sets), max(10, steps // 4), warmup)
+    return dict(ms_f=ms_f, ms_c=ms_c)
 
 
 def bench_conv(ops, dev, steps, warmup):
@@ -401,6 +429,7 @@ def main():
         dec = bench_decode(ops, dev, max(20, args.steps // 4), args.warmup)
         var = bench_varlen(ops, dev, max(10, args.steps // 10), 5)
         cv = bench_conv(ops, dev, args.steps, args.warmup)
+        fu = bench_fused(ops, dev, args.steps, args.warmup)
         line["secondary"] = {
             "gated_rmsnorm_1141x32x128": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                                  "hbm_frac": round(nrm["frac"], 4)},
@@ -412,6 +441,8 @@ def main():
             "causal_conv1d_silu_1141x8192_k4": {"us": round(cv["ms"] * 1e3, 2),
                                                 "GB/s": round(cv["gbs"], 1),
                                                 "hbm_frac": round(cv["frac"], 4)},
+            "fused_prefill_fp16_raw_T1141_HV32": {"us": round(fu["ms_f"] * 1e3, 2),
+                                                  "adapter_chain_us": round(fu["ms_c"] * 1e3, 2)},
             "causal_conv1d_update_B64x8192_k4": {"us": round(cv["ms_d"] * 1e3, 2),
                                                  "GB/s": round(cv["gbs_d"], 1),
                                                  "hbm_frac": round(cv["frac_d"], 4)},

@@ -92,6 +92,29 @@ hipError_t deltanet_tcop_chunk_prefill(const void* q, const void* k, const void*
                                        void* workspace, size_t workspace_bytes,
                                        hipStream_t stream, int dump_debug);
 
+/* Fused prefill on raw inputs.  Replaces the reference's TensorRT adapter
+ * runGdnChunkPrefillSm87 (export/patches/orin_text_engine/files/cpp/kernels/
+ * gdnKernels/gdnChunkPrefillSm87.cu:189-316), which runs separate kernels for
+ * the q/k L2 norm, the fp16 -> bf16 conversions, the gate math, the prefill,
+ * the bf16 -> fp16 conversion of o and a copy of the final state; here the
+ * prefill's two kernels do all of it while loading and storing.
+ *   q, k    : [B, T, HQK, 128] raw (not normalised); each row is scaled by
+ *             rsqrt(sum x^2 + 1e-6) in fp32 and rounded to bf16
+ *   v       : [B, T, HV, 128] (rounded to bf16)
+ *   a, b    : [B, T, HV]; A_log: fp32 [HV]; dt_bias: [HV]
+ *             g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b), fp32
+ *   o       : [B, T, HV, 128] (out; the bf16-rounded value)
+ *   state   : fp32 [B, HV, 128, 128], the initial state on entry and the
+ *             final state on return (the adapter's h0_source)
+ * q, k, v, a, b, dt_bias and o share io_dtype (GDN_DTYPE_FP16 as in the
+ * plugin, or GDN_DTYPE_BF16).  The workspace is deltanet_prefill_workspace_size
+ * bytes for the same B, T, HV. */
+hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k, const void* v,
+                                        const void* a, const void* b, const float* A_log,
+                                        const void* dt_bias, void* o, float* state, int B, int T,
+                                        int HV, int HQK, int io_dtype, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream);
+
 /* Variable-length prefill (no counterpart in the reference kernel: its torch
  * fallback drops cu_seqlens, transformers modeling_qwen3_5.py:259).
  * q, k, v, g, beta, o are packed [1, total_tokens, H, D]; cu_seqlens is a

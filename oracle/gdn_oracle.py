@@ -19,6 +19,8 @@ transformers 5.14.1 ``models/qwen3_5/modeling_qwen3_5.py``:
 * ``causal_conv1d_update``   -> modeling_qwen3_5.py:199-216
 * ``gdn_gate``               -> export/patches/orin_text_engine/files/cpp/kernels/
                                 gdnKernels/gdnChunkPrefillSm87.cu:113-125
+* ``fused_prefill``          -> gdnChunkPrefillSm87.cu:189-316 (runGdnChunkPrefillSm87:
+                                l2norm + conversions + gates + prefill + o / state out)
 * GQA head map               -> kernels/chunk_delta_cuda.h:12-14 (repeat_interleave)
 * tail padding               -> kernels/chunk_delta_cuda.cu:17-19
 
@@ -55,6 +57,7 @@ __all__ = [
     "unit_lower_inverse",
     "causal_conv1d",
     "causal_conv1d_update",
+    "fused_prefill",
 ]
 
 
@@ -329,3 +332,25 @@ def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
     win = torch.cat([conv_state, x], dim=-1).to(weight.dtype)
     new_state = win[:, :, -L:].to(conv_state.dtype)
     return _conv_valid(win, weight, bias, activation, T).to(x.dtype), new_state
+
+
+def fused_prefill(q, k, v, a, b, A_log, dt_bias, state, chunk_size=64, dtype=torch.float32):
+    """The reference TensorRT adapter's GDN step on raw inputs
+    (gdnChunkPrefillSm87.cu:189-316): q and k rows L2-normalised in fp32
+    with eps inside the rsqrt and rounded to bf16 (:52-84, :241-254), v
+    rounded to bf16 (:87-97, :257-261), g and beta from the gate inputs in
+    fp32 (:113-125), the prefill on those values, o rounded to bf16 and
+    returned in q's dtype (:292-303), the final state in place of the
+    initial one (:305-311).
+
+    q, k: [B, T, HK, 128]; v: [B, T, HV, 128]; a, b: [B, T, HV];
+    A_log, dt_bias: [HV]; state: [B, HV, 128, 128] (initial).
+    Returns (o, final_state); o rounded as the adapter rounds it, the state
+    in ``dtype``.
+    """
+    qn = l2norm(q.float()).to(torch.bfloat16)
+    kn = l2norm(k.float()).to(torch.bfloat16)
+    vb = v.to(torch.bfloat16)
+    g, beta = gdn_gate(a, b, A_log, dt_bias)
+    o, S = chunk_gated_delta_rule(qn, kn, vb, g, beta, state, chunk_size=chunk_size, dtype=dtype)
+    return o.to(torch.bfloat16).to(q.dtype), S

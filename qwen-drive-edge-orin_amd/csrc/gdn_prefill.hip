@@ -23,15 +23,18 @@
 //         W, decayed K^T and M as fp16 MFMA A-operand fragments and U as
 //         fp16 accumulator fragments, so the scan moves each operand with
 //         one 16-byte transfer per lane and never reshuffles.
-//   scan  one work-group per (state slice, v-head, sequence): the state of a
-//         head is split into 8 slices of 16 value columns, which evolve
-//         independently.  Wave 0 runs the serial chain with its 128x16 fp32
-//         slice in registers; it streams W, K~^T and U for chunk c+2 into a
-//         3-stage LDS ring with LDS-direct loads while computing chunk c.
-//         Six output waves take every sixth chunk and form
-//         O = (s e^c Q) S + M V_n from S and V_n handed over through LDS
-//         slots guarded by counters; each has six chain steps to cover its
-//         own load latency, so the chain never waits for outputs.
+//   scan  one work-group per (one or two state slices, v-head, sequence):
+//         the state of a head is split into 8 slices of 16 value columns,
+//         which evolve independently.  A chain wave per slice keeps its
+//         128x16 fp32 slice in registers; three loader waves stream W, K~^T
+//         and U into a 3-stage LDS ring; three output waves take every third
+//         chunk and form O = (s e^c Q) S + M V_n from S and V_n handed over
+//         through LDS slots guarded by counters.
+//
+// The fused entry (deltanet_chunk_prefill_fused) runs the same two kernels
+// on raw inputs: the prep L2-normalises q and k rows, converts fp16 v to
+// bf16 and forms g and beta from the gate inputs as it loads them, and the
+// scan stores o in the I/O dtype and the final state over the initial one.
 #include "gdn_common.h"
 #include "gdn_hip.h"
 
@@ -64,6 +67,22 @@ struct Workspace {
     float* dbgT;   // optional: T = (I-A)^-1, [chunk-head][64][64]
     float* dbgA;   // optional: A, same layout
     float* dbgC;   // optional: in-chunk cumsum of g, [chunk-head][64]
+};
+
+// Inputs of the prep kernel.  kRaw = 0: q, k (L2-normalised) and v are bf16,
+// g and beta fp32.  kRaw = 1 / 2: q, k, v are raw bf16 / fp16, and the gates
+// come from a, b (per token and v-head, same dtype), A_log (fp32) and dt_bias
+// (same dtype) per v-head.
+struct PrepIn {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const float* g;
+    const float* beta;
+    const uint16_t* a;
+    const uint16_t* b;
+    const float* A_log;
+    const uint16_t* dt_bias;
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -238,6 +257,39 @@ __device__ inline bf16x8 selector_frag(int h, int lg, int lm) {
     return e;
 }
 
+// A raw 16-bit input element as fp32 (kRaw 1: bf16, 2: fp16)
+template <int kRaw>
+__device__ inline float raw16(uint32_t bits) {
+    if constexpr (kRaw == 2) return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+    return __uint_as_float(bits << 16);
+}
+
+// The fused entry's gate math (export/patches/orin_text_engine/files/cpp/
+// kernels/gdnKernels/gdnChunkPrefillSm87.cu:44-49,113-125): g = -e^{A_log}
+// softplus(a + dt_bias), softplus(x) = x above 20, else log1p(e^x); and
+// beta = 1 / (1 + e^-b), all in fp32.
+__device__ inline void gate_from_raw(float a, float b, float A_log, float dt_bias, float& g,
+                                     float& beta) {
+    const float x = a + dt_bias;
+    g = -expf(A_log) * (x > 20.f ? x : log1pf(expf(x)));
+    beta = 1.f / (1.f + expf(-b));
+}
+
+// n L2-normalised 16-bit values (fp32 sum of squares already reduced to
+// `ss`), rounded to bf16 and packed in pairs: x rsqrt(ss + 1e-6), the
+// reference adapter's normalisation (gdnChunkPrefillSm87.cu:52-84).
+template <int kRaw>
+__device__ inline uint32_t norm_pair(uint32_t w, float inv) {
+    const float lo = raw16<kRaw>(w & 0xffffu) * inv, hi = raw16<kRaw>(w >> 16) * inv;
+    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+template <int kRaw>
+__device__ inline float sumsq_pair(uint32_t w, float s) {
+    const float lo = raw16<kRaw>(w & 0xffffu), hi = raw16<kRaw>(w >> 16);
+    return fmaf(hi, hi, fmaf(lo, lo, s));
+}
+
 // KK^T and KQ^T products of wave W: A column block W (row tiles W..3) and
 // M^T column block W (row tiles 0..W), k-blocks outermost so the five
 // accumulators' products interleave instead of waiting on each other.
@@ -258,13 +310,14 @@ __device__ inline void am_products(const bf16x8 (&ka)[4][4], const bf16x8 (&qf)[
     }
 }
 
-template <bool kDbg>
+template <bool kDbg, int kRaw>
 __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const float* __restrict__ g,
-    const float* __restrict__ beta, const int32_t* __restrict__ cu, int N, int T, int HV,
-    int HK, int nch_bound, float scale, Workspace ws) {
+    PrepIn in, const int32_t* __restrict__ cu, int N, int T, int HV, int HK, int nch_bound,
+    float scale, Workspace ws) {
     __shared__ PrepSmem sm;
+    const uint16_t* __restrict__ q = in.q;
+    const uint16_t* __restrict__ k = in.k;
+    const uint16_t* __restrict__ v = in.v;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lg = lane >> 4, lm = lane & 15;
@@ -292,9 +345,14 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     // gates need them before anything else arrives.
     float gv = 0.f, bv = 0.f;
     if (wave == 0) {
-        const int r = min(lane, rows - 1);
-        gv = g[(size_t)(tok0 + r) * HV + hv];
-        bv = beta[(size_t)(tok0 + r) * HV + hv];
+        const size_t gi = (size_t)(tok0 + min(lane, rows - 1)) * HV + hv;
+        if constexpr (kRaw == 0) {
+            gv = in.g[gi];
+            bv = in.beta[gi];
+        } else {
+            gate_from_raw(raw16<kRaw>(in.a[gi]), raw16<kRaw>(in.b[gi]), in.A_log[hv],
+                          raw16<kRaw>(in.dt_bias[hv]), gv, bv);
+        }
     }
     // K rows (16-byte pieces, row-major, bf16) go to LDS: thread t copies
     // pieces t, t + 256, ... (row piece / 16, columns 8 (piece % 16) ..).
@@ -329,6 +387,55 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
             const uint16_t* vrow = vs + (size_t)(tok0 + min(16 * tt + lm, rows - 1)) * HV * kDV;
             vr[tt][0] = *reinterpret_cast<const uint2*>(vrow);
             vr[tt][1] = *reinterpret_cast<const uint2*>(vrow + 16);
+        }
+    }
+
+    if constexpr (kRaw != 0) {
+        // raw inputs: K rows (16 lanes per row, 8 values each) and Q rows (4
+        // lanes per row, 32 values each) L2-normalised and rounded to bf16;
+        // fp16 V rounded to bf16
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            float ss = 0.f;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) ss = sumsq_pair<kRaw>(raw[ii][p], ss);
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
+            const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) raw[ii][p] = norm_pair<kRaw>(raw[ii][p], inv);
+        }
+        {
+            float ss = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    ss = sumsq_pair<kRaw>(qr[kb][h2].x, ss);
+                    ss = sumsq_pair<kRaw>(qr[kb][h2].y, ss);
+                }
+            }
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
+            const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    qr[kb][h2].x = norm_pair<kRaw>(qr[kb][h2].x, inv);
+                    qr[kb][h2].y = norm_pair<kRaw>(qr[kb][h2].y, inv);
+                }
+            }
+        }
+        if constexpr (kRaw == 2) {
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    vr[tt][h2].x = norm_pair<kRaw>(vr[tt][h2].x, 1.0f);
+                    vr[tt][h2].y = norm_pair<kRaw>(vr[tt][h2].y, 1.0f);
+                }
+            }
         }
     }
 
@@ -799,9 +906,13 @@ __device__ void run_loader(ScanSmem<SPW>& sm, const Workspace& ws, int chunk0, i
     }
 }
 
-template <int SPW>
+// kOutF16: o is stored as fp16 (the bf16-rounded value, converted exactly),
+// else bf16.  s0 and sf may be the same buffer: a chain reads its slice of
+// the initial state before its first chunk and writes the same elements
+// after its last, and no other wave touches either.
+template <int SPW, bool kOutF16>
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
-    Workspace ws, uint16_t* __restrict__ o, const float* __restrict__ s0, float* __restrict__ sf,
+    Workspace ws, uint16_t* __restrict__ o, const float* s0, float* sf,
     const int32_t* __restrict__ cu, int N, int T, int HV, int HK) {
     using Cfg = ScanCfg<SPW>;
     constexpr int kStageFrags = Cfg::kStageFrags;
@@ -1027,13 +1138,19 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
             // stores: lane (g, l) holds token 16 mt + l, columns 16 s2 + 4g ..
             // + 3 (one 8-byte write each); lane l then writes row l in
             // 8-column pieces
+            auto out16 = [](float x) -> uint32_t {
+                const uint32_t bb = f32_to_bf16_bits(x);
+                if constexpr (kOutF16)
+                    return __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(bb << 16));
+                return bb;
+            };
 #pragma unroll
             for (int s2 = 0; s2 < SPW; ++s2) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) {
                     uint2 pk;
-                    pk.x = (uint32_t)f32_to_bf16_bits(ov[s2][mt][0]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][1]) << 16);
-                    pk.y = (uint32_t)f32_to_bf16_bits(ov[s2][mt][2]) | ((uint32_t)f32_to_bf16_bits(ov[s2][mt][3]) << 16);
+                    pk.x = out16(ov[s2][mt][0]) | (out16(ov[s2][mt][1]) << 16);
+                    pk.y = out16(ov[s2][mt][2]) | (out16(ov[s2][mt][3]) << 16);
                     *reinterpret_cast<uint2*>(&ot[mt * 16 + lm][s2 * kBV + 4 * lg]) = pk;
                 }
             }
@@ -1050,8 +1167,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     // SIMD, so the chain keeps its SIMD to itself
 }
 
-hipError_t launch_prefill(const void* q, const void* k, const void* v, const float* g,
-                          const float* beta, void* o, const float* s0, float* sf,
+// raw: 0 for prepared inputs, 1 / 2 for the fused entry's raw bf16 / fp16
+// inputs (then o has that dtype too).
+hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
                           hipStream_t stream, int dump_debug, hipEvent_t* ev = nullptr,
@@ -1077,10 +1195,11 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     if (nch_bound > 0 && total_tokens > 0 && only != 1) {
         const int rep = HV / HK;
         const size_t groups = (nch_bound * (size_t)HK + 7) / 8;
-        hipLaunchKernelGGL(dump_debug ? gdn_prep_kernel<true> : gdn_prep_kernel<false>, dim3((unsigned)(groups * 8 * rep)), dim3(kPrepThreads),
-                           0, stream, static_cast<const uint16_t*>(q),
-                           static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), g,
-                           beta, cu, N, T, HV, HK, (int)nch_bound, scale, ws);
+        auto kern = raw == 1 ? gdn_prep_kernel<false, 1>
+                    : raw == 2 ? gdn_prep_kernel<false, 2>
+                    : dump_debug ? gdn_prep_kernel<true, 0> : gdn_prep_kernel<false, 0>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)(groups * 8 * rep)), dim3(kPrepThreads), 0, stream,
+                           in, cu, N, T, HV, HK, (int)nch_bound, scale, ws);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
@@ -1094,14 +1213,13 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 0;   // unknown: two slices per group
-    if ((long)groups * 8 * kSlicesPerHead <= (long)cus)
-        hipLaunchKernelGGL(gdn_scan_kernel<1>, dim3((unsigned)(groups * 8 * ScanCfg<1>::kGroupsPerHead)),
-                           dim3(kScanThreads), 0, stream, ws, static_cast<uint16_t*>(o), s0, sf, cu,
-                           N, T, HV, HK);
-    else
-        hipLaunchKernelGGL(gdn_scan_kernel<2>, dim3((unsigned)(groups * 8 * ScanCfg<2>::kGroupsPerHead)),
-                           dim3(kScanThreads), 0, stream, ws, static_cast<uint16_t*>(o), s0, sf, cu,
-                           N, T, HV, HK);
+    const bool one = (long)groups * 8 * kSlicesPerHead <= (long)cus;
+    const bool f16 = raw == 2;
+    auto scan = one ? (f16 ? gdn_scan_kernel<1, true> : gdn_scan_kernel<1, false>)
+                    : (f16 ? gdn_scan_kernel<2, true> : gdn_scan_kernel<2, false>);
+    const int gph = one ? ScanCfg<1>::kGroupsPerHead : ScanCfg<2>::kGroupsPerHead;
+    hipLaunchKernelGGL(scan, dim3((unsigned)(groups * 8 * gph)), dim3(kScanThreads), 0, stream, ws,
+                       static_cast<uint16_t*>(o), s0, sf, cu, N, T, HV, HK);
     hipError_t err = hipGetLastError();
     if (ev) (void)hipEventRecord(ev[2], stream);
     return err;
@@ -1109,6 +1227,16 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, const flo
 
 constexpr int kPrefillKernels = 2;
 const char* const kPrefillKernelNames[kPrefillKernels] = {"gdn_prep_kernel", "gdn_scan_kernel"};
+
+PrepIn plain_in(const void* q, const void* k, const void* v, const float* g, const float* beta) {
+    PrepIn in{};
+    in.q = static_cast<const uint16_t*>(q);
+    in.k = static_cast<const uint16_t*>(k);
+    in.v = static_cast<const uint16_t*>(v);
+    in.g = g;
+    in.beta = beta;
+    return in;
+}
 
 bool dims_ok(int HV, int HQK, int DK, int DV, int chunk_size) {
     return DK == kDK && DV == kDV && chunk_size == kChunk && HQK > 0 && HV > 0 && HV % HQK == 0;
@@ -1137,8 +1265,8 @@ extern "C" hipError_t deltanet_chunk_prefill(const void* q, const void* k, const
     if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
     if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
-    return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
-                          HV, HQK, nc, workspace, workspace_bytes, stream, dump_debug);
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
+                          T, B * T, HV, HQK, nc, workspace, workspace_bytes, stream, dump_debug);
 }
 
 extern "C" int deltanet_prefill_kernel_count(void) { return kPrefillKernels; }
@@ -1162,8 +1290,8 @@ extern "C" hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k,
     if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
     if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
-    return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
-                          HV, HQK, nc, workspace, workspace_bytes, stream, 0, events);
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
+                          T, B * T, HV, HQK, nc, workspace, workspace_bytes, stream, 0, events);
 }
 
 extern "C" hipError_t deltanet_chunk_prefill_kernel(const void* q, const void* k, const void* v,
@@ -1178,8 +1306,9 @@ extern "C" hipError_t deltanet_chunk_prefill_kernel(const void* q, const void* k
     if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
     if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
-    return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, nullptr, B, T, B * T,
-                          HV, HQK, nc, workspace, workspace_bytes, stream, 0, nullptr, kernel);
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
+                          T, B * T, HV, HQK, nc, workspace, workspace_bytes, stream, 0, nullptr,
+                          kernel);
 }
 
 extern "C" size_t deltanet_prefill_varlen_workspace_size(int total_tokens, int num_seqs, int HV,
@@ -1202,9 +1331,9 @@ extern "C" hipError_t deltanet_chunk_prefill_varlen(
     if (!cu_seqlens || !workspace || !final_state) return hipErrorInvalidValue;
     if (total_tokens > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
     const size_t nc = ((size_t)total_tokens + (size_t)(kChunk - 1) * num_seqs) / kChunk;
-    return launch_prefill(q, k, v, g, beta, o, initial_state, final_state, cu_seqlens, num_seqs,
-                          0, total_tokens, HV, HQK, nc, workspace, workspace_bytes, stream,
-                          dump_debug);
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, cu_seqlens,
+                          num_seqs, 0, total_tokens, HV, HQK, nc, workspace, workspace_bytes,
+                          stream, dump_debug);
 }
 
 // Twins of the reference's bf16-wmma o-pass variant (kernels/chunk_delta_cuda_tco.h);
@@ -1224,4 +1353,28 @@ extern "C" hipError_t deltanet_tcop_chunk_prefill(const void* q, const void* k, 
     return deltanet_chunk_prefill(q, k, v, g, beta, o, initial_state, final_state, B, T, HV, HQK,
                                   DK, DV, chunk_size, workspace, workspace_bytes, stream,
                                   dump_debug);
+}
+
+extern "C" hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k, const void* v,
+                                                   const void* a, const void* b,
+                                                   const float* A_log, const void* dt_bias,
+                                                   void* o, float* state, int B, int T, int HV,
+                                                   int HQK, int io_dtype, void* workspace,
+                                                   size_t workspace_bytes, hipStream_t stream) {
+    if (!dims_ok(HV, HQK, kDK, kDV, kChunk) || B <= 0 || T < 0) return hipErrorInvalidValue;
+    if (io_dtype != GDN_DTYPE_BF16 && io_dtype != GDN_DTYPE_FP16) return hipErrorInvalidValue;
+    if (workspace == nullptr || state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !a || !b || !A_log || !dt_bias || !o))
+        return hipErrorInvalidValue;
+    PrepIn in{};
+    in.q = static_cast<const uint16_t*>(q);
+    in.k = static_cast<const uint16_t*>(k);
+    in.v = static_cast<const uint16_t*>(v);
+    in.a = static_cast<const uint16_t*>(a);
+    in.b = static_cast<const uint16_t*>(b);
+    in.A_log = A_log;
+    in.dt_bias = static_cast<const uint16_t*>(dt_bias);
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    return launch_prefill(in, io_dtype == GDN_DTYPE_FP16 ? 2 : 1, o, state, state, nullptr, B, T,
+                          B * T, HV, HQK, nc, workspace, workspace_bytes, stream, 0);
 }

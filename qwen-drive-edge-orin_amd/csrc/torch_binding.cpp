@@ -9,7 +9,8 @@
 // libgdn_hip.so (include/gdn_hip.h) with raw pointers; no torch types cross
 // that boundary.  New relative to the reference: a trailing keyword
 // `cu_seqlens` (varlen prefill), `recurrent_step` (decode),
-// `gated_rmsnorm` and the causal conv1d ops `causal_conv1d_fwd` /
+// `gated_rmsnorm`, `chunk_prefill_fused` (the TensorRT adapter's whole GDN
+// step on raw inputs) and the causal conv1d ops `causal_conv1d_fwd` /
 // `causal_conv1d_update` that produce q/k/v upstream of the recurrence.
 #include <torch/extension.h>
 
@@ -18,6 +19,7 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <algorithm>
 #include <optional>
 #include <vector>
 
@@ -214,6 +216,57 @@ at::Tensor gated_rmsnorm(at::Tensor x, at::Tensor z, at::Tensor weight, double e
     return y;
 }
 
+// The reference TensorRT adapter's whole GDN step on raw inputs
+// (gdnChunkPrefillSm87.cu:189-316) as one op: q, k [B, T, HQK, 128] raw;
+// v [B, T, HV, 128]; a, b [B, T, HV]; A_log [HV] (fp32); dt_bias [HV];
+// state [B, HV, 128, 128] fp32, initial on entry, final on return.  q, k,
+// v, a, b, dt_bias share one dtype (fp16 or bf16), which o gets too.
+at::Tensor chunk_prefill_fused(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor a,
+                               at::Tensor b, at::Tensor A_log, at::Tensor dt_bias,
+                               at::Tensor state) {
+    for (const at::Tensor* t : {&q, &k, &v, &a, &b, &A_log, &dt_bias, &state})
+        TORCH_CHECK(t->is_cuda(), "all inputs must be CUDA tensors");
+    const auto dt = q.scalar_type();
+    TORCH_CHECK(dt == at::kHalf || dt == at::kBFloat16, "q must be fp16 or bf16");
+    TORCH_CHECK(k.scalar_type() == dt && v.scalar_type() == dt && a.scalar_type() == dt &&
+                    b.scalar_type() == dt && dt_bias.scalar_type() == dt,
+                "q, k, v, a, b and dt_bias must share one dtype");
+    TORCH_CHECK(A_log.scalar_type() == at::kFloat, "A_log must be fp32");
+    TORCH_CHECK(state.scalar_type() == at::kFloat && state.is_contiguous(),
+                "state must be a contiguous fp32 tensor (updated in place)");
+    TORCH_CHECK(q.dim() == 4 && k.sizes() == q.sizes() && v.dim() == 4 && a.dim() == 3 &&
+                    b.sizes() == a.sizes(),
+                "bad ranks or shapes");
+    const int64_t B = q.size(0), T = q.size(1), HQK = q.size(2), HV = v.size(2);
+    TORCH_CHECK(q.size(3) == 128 && v.size(3) == 128, "only head dims of 128 are supported");
+    TORCH_CHECK(v.size(0) == B && v.size(1) == T && a.size(0) == B && a.size(1) == T &&
+                    a.size(2) == HV,
+                "batch/time/head mismatch");
+    TORCH_CHECK(HV % HQK == 0, "HV must be a multiple of HQK");
+    TORCH_CHECK(A_log.numel() == HV && dt_bias.numel() == HV, "A_log and dt_bias must be [HV]");
+    TORCH_CHECK(state.dim() == 4 && state.size(0) == B && state.size(1) == HV &&
+                    state.size(2) == 128 && state.size(3) == 128,
+                "state must be [B, HV, 128, 128]");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
+    auto ac = a.contiguous(), bc = b.contiguous();
+    auto Ac = A_log.contiguous(), dc = dt_bias.contiguous();
+    auto o = at::empty_like(vc);
+    const size_t ws_bytes =
+        deltanet_prefill_workspace_size((int)B, (int)T, (int)HV, 128, 128, kChunk);
+    TORCH_CHECK(ws_bytes > 0 || T == 0, "unsupported prefill configuration");
+    auto ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 256)}, vc.options().dtype(at::kByte));
+    check_hip(deltanet_chunk_prefill_fused(
+                  qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), ac.data_ptr(), bc.data_ptr(),
+                  Ac.data_ptr<float>(), dc.data_ptr(), o.data_ptr(), state.data_ptr<float>(),
+                  (int)B, (int)T, (int)HV, (int)HQK,
+                  dt == at::kHalf ? GDN_DTYPE_FP16 : GDN_DTYPE_BF16, ws.data_ptr(),
+                  (size_t)ws.numel(),
+                  current_stream()),
+              "deltanet_chunk_prefill_fused");
+    return o;
+}
+
 int conv_io_dtype(const at::Tensor& x) {
     TORCH_CHECK(x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf,
                 "x must be bf16 or fp16");
@@ -308,6 +361,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("recurrent_step", &recurrent_step,
           "recurrent gated delta rule (decode), state updated in place; returns o", "q"_a, "k"_a,
           "v"_a, "g"_a, "beta"_a, "state"_a);
+    m.def("chunk_prefill_fused", &chunk_prefill_fused,
+          "prefill on raw inputs (q/k L2 norm, gates, dtype conversions fused); state updated "
+          "in place; returns o",
+          "q"_a, "k"_a, "v"_a, "a"_a, "b"_a, "A_log"_a, "dt_bias"_a, "state"_a);
     m.def("gated_rmsnorm", &gated_rmsnorm, "y = rmsnorm(x) * weight * silu(z)", "x"_a, "z"_a,
           "weight"_a, "eps"_a = 1e-6);
     m.def("causal_conv1d_fwd", &causal_conv1d_fwd,

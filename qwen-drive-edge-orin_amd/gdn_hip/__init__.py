@@ -11,6 +11,8 @@ The compiled pieces live next to this file:
   chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None) -> [o, final_state]
   chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
   recurrent_step(q, k, v, g, beta, state) -> o          (state updated in place)
+  chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state) -> o
+                          raw q/k/v and gate inputs     (state updated in place)
   gated_rmsnorm(x, z, weight, eps=1e-6) -> y
   causal_conv1d_fwd(x, weight, bias=None, silu=False) -> y      x, y [B, D, T]
   causal_conv1d_update(x, conv_state, weight, bias=None, silu=False) -> y
@@ -55,6 +57,10 @@ def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
 
 def chunk_prefill_debug(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
     return load().chunk_prefill_debug(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens)
+
+
+def chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state):
+    return load().chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state)
 
 
 def recurrent_step(q, k, v, g, beta, state):

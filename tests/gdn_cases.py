@@ -169,3 +169,22 @@ def flops_prefill(total_tokens, hv):
 
 
 assert math.isclose(flops_prefill(1, 1), 182954.67, rel_tol=1e-6)
+
+
+def fused_inputs(seed, B, T, HK, HV, D=128, dtype=torch.float16, s0_scale=0.02):
+    """Raw inputs of the fused prefill (gdnChunkPrefillSm87.cu:189-316): raw
+    (unnormalised) q/k rows, v, gate inputs a, b, per-head A_log and dt_bias,
+    an initial state.  A = e^{A_log} in U(0.02, 1) and dt_bias in N(0, 0.5)
+    keep the per-token decay g in the range of the other prefill cases
+    (mostly -0.05 .. -2); a freshly initialised layer's A = U(0, 16) would
+    decay every state to ~0 within a token."""
+    gen = _gen(seed)
+    q = torch.randn(B, T, HK, D, generator=gen).to(dtype)
+    k = torch.randn(B, T, HK, D, generator=gen).to(dtype)
+    v = torch.randn(B, T, HV, D, generator=gen).to(dtype)
+    a = torch.randn(B, T, HV, generator=gen).to(dtype)
+    b = torch.randn(B, T, HV, generator=gen).to(dtype)
+    A_log = torch.log(0.02 + 0.98 * torch.rand(HV, generator=gen))
+    dt_bias = (0.5 * torch.randn(HV, generator=gen)).to(dtype)
+    s0 = s0_scale * torch.randn(B, HV, D, D, generator=gen)
+    return q, k, v, a, b, A_log, dt_bias, s0

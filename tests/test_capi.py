@@ -124,6 +124,26 @@ def test_decode_and_norm_reject_on_host(lib):
     assert nrm(None, 1, 1, 1, 10, 128, 1e-6, capi.DTYPE_BF16, capi.DTYPE_BF16, None) == INVALID
 
 
+def test_fused_prefill_rejects_on_host(lib):
+    f = lib.deltanet_chunk_prefill_fused
+    # q, k, v, a, b, A_log, dt_bias, o, state, B, T, HV, HQK, io dtype, ws, ws bytes, stream
+    ok = [1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 4, 2, capi.DTYPE_FP16, 1, 1 << 40, None]
+
+    def c(**over):
+        a = list(ok)
+        for i, v in over.items():
+            a[int(i[1:])] = v
+        return f(*a)
+
+    assert c(a13=capi.DTYPE_FP32) == INVALID                 # fp32 I/O
+    assert c(a12=3) == INVALID                               # HV % HQK
+    assert c(a8=None) == INVALID                             # no state
+    assert c(a3=None) == INVALID and c(a5=None) == INVALID and c(a6=None) == INVALID
+    assert c(a14=None) == INVALID
+    assert c(a15=16) == INVALID                              # short workspace
+    assert c(a9=0) == INVALID
+
+
 def test_conv_reject_on_host(lib):
     fwd = lib.gdn_causal_conv1d_fwd
     bf, fp32 = capi.DTYPE_BF16, capi.DTYPE_FP32
@@ -167,7 +187,7 @@ def test_torch_extension_loads_and_checks_device():
 
     ops = gdn_hip.load()
     for name in ("chunk_prefill", "chunk_prefill_debug", "recurrent_step", "gated_rmsnorm",
-                 "causal_conv1d_fwd", "causal_conv1d_update"):
+                 "chunk_prefill_fused", "causal_conv1d_fwd", "causal_conv1d_update"):
         assert hasattr(ops, name)
     q = torch.zeros(1, 64, 2, 128, dtype=torch.bfloat16)
     v = torch.zeros(1, 64, 4, 128, dtype=torch.bfloat16)

@@ -413,3 +413,47 @@ def test_conv_pins_detect_planted_mistakes(mutation):
     xb, wb, bb = _conv_inputs(81, torch.bfloat16, torch.bfloat16)
     tf_equal = torch.equal(_mutant_conv(xb, wb, bb, "silu", mutation), fn(xb, wb, bb, "silu"))
     assert brute_err > 1e-3 or not tf_equal, f"pins missed planted mistake {mutation}"
+
+
+# ---------------------------------------------------- fused prefill (f2)
+
+
+def test_fused_prefill_power_of_two_row_scales_are_invisible():
+    # x 2^s changes neither the normalised rows (exact scaling; the sums of
+    # squares stay far above the 1e-6 eps) nor anything downstream: pins
+    # that q and k are normalised before use
+    q, k, v, a, b, A_log, dt_bias, s0 = gc.fused_inputs(90, B=1, T=70, HK=2, HV=4, D=32)
+    o1, S1 = orc.fused_prefill(q, k, v, a, b, A_log, dt_bias, s0)
+    o2, S2 = orc.fused_prefill(q * 4, k * 0.5, v, a, b, A_log, dt_bias, s0)
+    assert torch.equal(o1, o2) and torch.equal(S1, S2)
+    o3, _ = orc.fused_prefill(q, k, v * 2, a, b, A_log, dt_bias, s0)
+    assert not torch.equal(o1, o3)                       # v is not normalised
+
+
+def test_fused_prefill_matches_transformers_l2norm_path():
+    # transformers' own prefill with use_qk_l2norm_in_kernel=True on the raw
+    # rows, gates from the same inputs; differences are the adapter's bf16
+    # roundings of q, k, v and o only
+    m = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    chunk = getattr(m.torch_chunk_gated_delta_rule, "__wrapped__", m.torch_chunk_gated_delta_rule)
+    q, k, v, a, b, A_log, dt_bias, s0 = gc.fused_inputs(91, B=1, T=150, HK=2, HV=2, D=128)
+    o, S = orc.fused_prefill(q, k, v, a, b, A_log, dt_bias, s0)
+    g, beta = orc.gdn_gate(a, b, A_log, dt_bias)
+    o_t, S_t = chunk(q.float(), k.float(), v.float(), g, beta, initial_state=s0,
+                     output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert _err(o, o_t) < 2e-2 and _err(S, S_t) < 2e-2
+    assert (o.double() - o_t.double()).norm() / o_t.double().norm() < 1e-2
+
+
+def test_fused_prefill_fp16_and_bf16_inputs_agree_on_shared_values():
+    # values representable in both dtypes give the same result; o is the
+    # bf16-rounded value, converted to fp16 for fp16 inputs (exact but for
+    # fp16 subnormals, |o| < 6.1e-5)
+    q, k, v, a, b, A_log, dt_bias, s0 = gc.fused_inputs(92, B=1, T=40, HK=1, HV=2, D=32)
+    r = lambda x: (x.float() * 8).round() / 8                  # noqa: E731  dyadic, |x| < 8
+    args16 = [r(t).to(torch.float16) for t in (q, k, v, a, b)]
+    args_b = [r(t).to(torch.bfloat16) for t in (q, k, v, a, b)]
+    o16, S16 = orc.fused_prefill(*args16, A_log, r(dt_bias).to(torch.float16), s0)
+    ob, Sb = orc.fused_prefill(*args_b, A_log, r(dt_bias).to(torch.bfloat16), s0)
+    assert o16.dtype == torch.float16 and ob.dtype == torch.bfloat16
+    assert torch.equal(o16, ob.to(torch.float16)) and torch.equal(S16, Sb)
