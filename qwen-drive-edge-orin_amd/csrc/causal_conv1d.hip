@@ -299,6 +299,113 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update_kernel(
     }
 }
 
+// The decode update for the Qwen3.5 shape (K = 4 taps, a state of 4
+// tokens): one thread per (batch, 4 consecutive channels), so the state (4
+// channels x 4 tokens, 32 bytes), the weights and a token of x or y each
+// move in one or two vector accesses.  Same arithmetic per channel as the
+// kernel above.  Requires unit channel strides for x and y, state rows of
+// exactly 4 tokens, and the alignments the launcher checks.
+template <int IO, int WT, bool SILU>
+__global__ __launch_bounds__(kConvThreads) void causal_conv1d_update4_kernel(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ state, const void* __restrict__ w,
+    const void* __restrict__ bias, uint16_t* __restrict__ y, int B, int T, int D, int64_t xbs,
+    int64_t xts, int64_t sbs, int64_t ybs, int64_t yts) {
+    const int64_t gid = (int64_t)blockIdx.x * kConvThreads + threadIdx.x;
+    const int D4 = D / 4;
+    if (gid >= (int64_t)B * D4) return;
+    const int b = (int)(gid / D4), d0 = 4 * (int)(gid - (int64_t)b * D4);
+    // weights [d0 .. d0+3][0..3] and bias
+    float wf[4][4], bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (WT == 2) {
+        const f32x4* wp = reinterpret_cast<const f32x4*>(static_cast<const float*>(w) + (size_t)d0 * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f32x4 r = wp[e];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wf[e][j] = r[j];
+        }
+        if (bias) {
+            const f32x4 r = *reinterpret_cast<const f32x4*>(static_cast<const float*>(bias) + d0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[e] = r[e];
+        }
+    } else {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w) + (size_t)d0 * 4);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x4 r = wp[h];   // channels 2h, 2h+1: taps 0..3 each
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                wf[2 * h + p / 2][2 * (p % 2)] = lo16<WT>(r[p]);
+                wf[2 * h + p / 2][2 * (p % 2) + 1] = hi16<WT>(r[p]);
+            }
+        }
+        if (bias) {
+            const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(bias) + d0);
+            bv[0] = lo16<WT>(r.x);
+            bv[1] = hi16<WT>(r.x);
+            bv[2] = lo16<WT>(r.y);
+            bv[3] = hi16<WT>(r.y);
+        }
+    }
+    // state rows: channel e's 4 tokens, oldest first, 8 bytes per channel
+    uint16_t* st = state + (size_t)b * sbs + (size_t)d0 * 4;
+    uint16_t win[4][4];   // [channel][slot]: the last 4 window tokens, oldest first
+    {
+        const u32x4 r0 = reinterpret_cast<const u32x4*>(st)[0];   // channels 0, 1
+        const u32x4 r1 = reinterpret_cast<const u32x4*>(st)[1];   // channels 2, 3
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const u32x4 r = e < 2 ? r0 : r1;
+            const uint32_t v = r[2 * (e % 2)], u = r[2 * (e % 2) + 1];
+            win[e][0] = (uint16_t)v;
+            win[e][1] = (uint16_t)(v >> 16);
+            win[e][2] = (uint16_t)u;
+            win[e][3] = (uint16_t)(u >> 16);
+        }
+    }
+    const uint16_t* xb = x + (size_t)b * xbs + d0;
+    uint16_t* yb = y + (size_t)b * ybs + d0;
+    for (int i = 0; i < T; ++i) {
+        const uint2 xr = *reinterpret_cast<const uint2*>(xb + (size_t)i * xts);
+        const uint16_t xe[4] = {(uint16_t)xr.x, (uint16_t)(xr.x >> 16), (uint16_t)xr.y,
+                                (uint16_t)(xr.y >> 16)};
+        uint32_t out[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // window slots 1..3 and the new token are the 4 taps, oldest first
+#pragma unroll
+            for (int j = 0; j < 3; ++j) win[e][j] = win[e][j + 1];
+            win[e][3] = xe[e];
+            float acc = fmaf(wf[e][0], cv_load<IO>(win[e][0]), 0.0f);
+#pragma unroll
+            for (int j = 1; j < 4; ++j) acc = fmaf(wf[e][j], cv_load<IO>(win[e][j]), acc);
+            if (bias) acc += bv[e];
+            out[e] = finish1<IO, WT, SILU>(acc);
+        }
+        uint2 yo;
+        yo.x = out[0] | (out[1] << 16);
+        yo.y = out[2] | (out[3] << 16);
+        *reinterpret_cast<uint2*>(yb + (size_t)i * yts) = yo;
+    }
+    // new state: the window's last 4 tokens per channel
+    u32x4 n0, n1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t v = (uint32_t)win[e][0] | ((uint32_t)win[e][1] << 16);
+        const uint32_t u = (uint32_t)win[e][2] | ((uint32_t)win[e][3] << 16);
+        if (e < 2) {
+            n0[2 * e] = v;
+            n0[2 * e + 1] = u;
+        } else {
+            n1[2 * (e - 2)] = v;
+            n1[2 * (e - 2) + 1] = u;
+        }
+    }
+    reinterpret_cast<u32x4*>(st)[0] = n0;
+    reinterpret_cast<u32x4*>(st)[1] = n1;
+}
+
 template <int IO, int WT, bool SILU, bool BIAS>
 hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, int B, int T, int D,
                       int K, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
@@ -354,6 +461,32 @@ hipError_t launch_update(const void* x, void* state, const void* w, const void* 
                          int B, int T, int D, int K, int state_len, int64_t xbs, int64_t xts,
                          int64_t xds, int64_t sbs, int64_t sds, int64_t ybs, int64_t yts,
                          int64_t yds, int silu, hipStream_t stream) {
+    // the vector path: K = 4, 4-token state rows, unit channel strides, and
+    // every vector access aligned (x, y: 8 bytes per 4 channels; state and
+    // weights: 16; bias: 8, or 16 in fp32)
+    const auto al = [](const void* p, uintptr_t a) {
+        return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+    };
+    if (K == 4 && state_len == 4 && sds == 4 && xds == 1 && yds == 1 && D % 4 == 0 &&
+        (B <= 1 || (xbs % 4 == 0 && ybs % 4 == 0 && sbs % 8 == 0)) &&
+        (T <= 1 || (xts % 4 == 0 && yts % 4 == 0)) && al(x, 8) && al(y, 8) && al(state, 16) &&
+        al(w, 16) && (!bias || al(bias, WT == 2 ? 16 : 8))) {
+        const int64_t n4 = (int64_t)B * (D / 4);
+        const dim3 grid4((unsigned)((n4 + kConvThreads - 1) / kConvThreads));
+        auto xp = static_cast<const uint16_t*>(x);
+        auto sp = static_cast<uint16_t*>(state);
+        auto yp = static_cast<uint16_t*>(y);
+        const int64_t xb = B <= 1 ? 0 : xbs, yb = B <= 1 ? 0 : ybs, sb = B <= 1 ? 0 : sbs;
+        if (silu)
+            hipLaunchKernelGGL((causal_conv1d_update4_kernel<IO, WT, true>), grid4,
+                               dim3(kConvThreads), 0, stream, xp, sp, w, bias, yp, B, T, D, xb,
+                               xts, sb, yb, yts);
+        else
+            hipLaunchKernelGGL((causal_conv1d_update4_kernel<IO, WT, false>), grid4,
+                               dim3(kConvThreads), 0, stream, xp, sp, w, bias, yp, B, T, D, xb,
+                               xts, sb, yb, yts);
+        return hipGetLastError();
+    }
     const int64_t n = (int64_t)B * D;
     const dim3 grid((unsigned)((n + kConvThreads - 1) / kConvThreads));
     auto xp = static_cast<const uint16_t*>(x);
