@@ -105,7 +105,10 @@ __global__ __launch_bounds__(kNormThreads) void gated_rmsnorm_kernel(
             const float n = round_io<IO>(xf[j] * r);
             float hv = wf[j] * n;
             if (W != 2) hv = round_io<IO>(hv);
-            const float sz = zf[j] / (1.0f + expf(-zf[j]));
+            // silu(z) = z / (1 + e^-z) from the hardware base-2 exponential
+            // and reciprocal (each within about an fp32 ulp)
+            const float sz = zf[j] * __builtin_amdgcn_rcpf(
+                                         1.0f + __builtin_amdgcn_exp2f(zf[j] * -1.44269504088896341f));
             pk |= store_elem<IO>(hv * sz) << (16 * h);
         }
         out[p] = pk;
