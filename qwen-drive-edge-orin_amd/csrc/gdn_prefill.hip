@@ -792,6 +792,7 @@ struct ScanSmem {
     int ready[SPW];                        // per chain: chunks whose hand-off part is written
     int cons[kHand];                       // per slot: 1 + the chunk an output wave last read from it
     int red[kScanThreads / 64];
+    int order[64];                         // varlen: sequences by length, longest first
 };
 
 __device__ __forceinline__ int lds_load_relaxed(const int* p) {
@@ -928,7 +929,25 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     const int sp = qd % Cfg::kGroupsPerHead;
     const int pair = (qd / Cfg::kGroupsPerHead) * 8 + xcd;
     if (pair >= N * HV) return;
-    const int seq = pair / HV, hv = pair - seq * HV;
+    int seq = pair / HV;
+    const int hv = pair - seq * HV;
+    // Packed sequences of different lengths: work-groups start in id order as
+    // CUs free up, so hand the low ids to the longest sequences (longest
+    // processing time first); a grid of more groups than CUs then ends close
+    // to total work / CUs instead of waiting on a long sequence started last.
+    if (cu && N <= 64) {
+        if (tid < N) {
+            const int my = cu[tid + 1] - cu[tid];
+            int rank = 0;
+            for (int u = 0; u < N; ++u) {
+                const int lu = cu[u + 1] - cu[u];
+                rank += (lu > my || (lu == my && u < tid)) ? 1 : 0;
+            }
+            sm.order[rank] = tid;
+        }
+        __syncthreads();
+        seq = sm.order[seq];
+    }
     const int hk = hv / (HV / HK);
     const int sl0 = SPW * sp;   // first slice of this group
 
