@@ -174,6 +174,38 @@ def bench_fused(ops, dev, steps, warmup):
     return dict(ms_f=ms_f, ms_c=ms_c)
 
 
+def bench_hf_lane(ops, dev, steps, warmup):
+    """transformers' call into the fla adapter at T=1141, HV=32 (q/k already
+    repeat_interleaved to 32 heads, bf16, use_qk_l2norm_in_kernel=True):
+    with the q/k normalisation in the prep kernel, and with it done by torch
+    first (the adapter's path for other dtypes or a custom scale)."""
+    import importlib
+    import torch
+    import gdn_cases as gc
+
+    hf = str(ROOT / "qwen-drive-edge-orin_amd" / "hf")
+    sys.path.insert(0, hf)
+    try:
+        ad = importlib.import_module("fla.ops.gated_delta_rule")
+    finally:
+        sys.path.remove(hf)
+    gen = torch.Generator().manual_seed(5)
+    T, HV = 1141, 32
+    q = torch.randn(1, T, HV, 128, generator=gen).bfloat16().to(dev)
+    k = torch.randn(1, T, HV, 128, generator=gen).bfloat16().to(dev)
+    _, _, v, g, beta, s0 = gc.prefill_inputs()
+    v, g, beta, s0 = v.to(dev), g.to(dev), beta.to(dev), s0.to(dev)
+    call = lambda i: ad.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0,  # noqa: E731
+                                               output_final_state=True,
+                                               use_qk_l2norm_in_kernel=True)
+    ms_k = time_calls(call, 1, max(10, steps // 4), warmup)
+    call_t = lambda i: ad.chunk_gated_delta_rule(q, k, v, g, beta, scale=0.0883883,  # noqa: E731
+                                                 initial_state=s0, output_final_state=True,
+                                                 use_qk_l2norm_in_kernel=True)
+    ms_t = time_calls(call_t, 1, max(10, steps // 4), warmup)
+    return dict(ms_k=ms_k, ms_t=ms_t)
+
+
 def bench_conv(ops, dev, steps, warmup):
     """Causal conv1d + SiLU ahead of the recurrence: the prefill form over
     the layer's conv channels (D = 2 * 16 * 128 + 32 * 128 = 8192, T = 1141,
@@ -430,6 +462,7 @@ def main():
         var = bench_varlen(ops, dev, max(10, args.steps // 10), 5)
         cv = bench_conv(ops, dev, args.steps, args.warmup)
         fu = bench_fused(ops, dev, args.steps, args.warmup)
+        hl = bench_hf_lane(ops, dev, args.steps, args.warmup)
         line["secondary"] = {
             "gated_rmsnorm_1141x32x128": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                                  "hbm_frac": round(nrm["frac"], 4)},
@@ -443,6 +476,9 @@ def main():
                                                 "hbm_frac": round(cv["frac"], 4)},
             "fused_prefill_fp16_raw_T1141_HV32": {"us": round(fu["ms_f"] * 1e3, 2),
                                                   "adapter_chain_us": round(fu["ms_c"] * 1e3, 2)},
+            "hf_lane_chunk_gated_delta_rule_T1141_HV32": {
+                "us": round(hl["ms_k"] * 1e3, 2),
+                "us_torch_l2norm": round(hl["ms_t"] * 1e3, 2)},
             "causal_conv1d_update_B64x8192_k4": {"us": round(cv["ms_d"] * 1e3, 2),
                                                  "GB/s": round(cv["gbs_d"], 1),
                                                  "hbm_frac": round(cv["frac_d"], 4)},

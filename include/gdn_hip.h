@@ -133,6 +133,21 @@ hipError_t deltanet_chunk_prefill_varlen(const void* q, const void* k, const voi
                                          size_t workspace_bytes, hipStream_t stream,
                                          int dump_debug);
 
+/* deltanet_chunk_prefill (cu_seqlens NULL: B sequences of T tokens) or
+ * deltanet_chunk_prefill_varlen (cu_seqlens set, B = 1, T = total tokens)
+ * with raw bf16 q and k rows, L2-normalised inside the prep kernel as
+ * x rsqrt(sum x^2 + 1e-6) in fp32 and rounded to bf16 -- transformers'
+ * use_qk_l2norm_in_kernel=True (models/qwen3_5/modeling_qwen3_5.py:242-245,
+ * 270-271).  No counterpart in the reference kernel, whose callers normalise
+ * first (kernels/chunk_delta_cuda.h:23-25).  Workspace as for the entry it
+ * mirrors. */
+hipError_t deltanet_chunk_prefill_l2norm(const void* q, const void* k, const void* v,
+                                         const float* g, const float* beta, void* o,
+                                         const float* initial_state, float* final_state,
+                                         const int32_t* cu_seqlens, int num_seqs, int B, int T,
+                                         int HV, int HQK, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream);
+
 /* Recurrent step (decode; T >= 1 tokens per sequence), state updated in
  * place.  Fused native form of the torch token recurrence the reference runs
  * for decode (transformers modeling_qwen3_5.py:331-380,

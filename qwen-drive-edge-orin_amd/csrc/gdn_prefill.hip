@@ -70,9 +70,10 @@ struct Workspace {
 };
 
 // Inputs of the prep kernel.  kRaw = 0: q, k (L2-normalised) and v are bf16,
-// g and beta fp32.  kRaw = 1 / 2: q, k, v are raw bf16 / fp16, and the gates
-// come from a, b (per token and v-head, same dtype), A_log (fp32) and dt_bias
-// (same dtype) per v-head.
+// g and beta fp32.  kRaw = 1 / 2: q and k rows are raw bf16 / fp16 (the prep
+// normalises them), v has the same dtype, and the gates are g and beta (fp32)
+// when `a` is null, else they come from a, b (per token and v-head, same
+// dtype), A_log (fp32) and dt_bias (same dtype) per v-head.
 struct PrepIn {
     const uint16_t* q;
     const uint16_t* k;
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     float gv = 0.f, bv = 0.f;
     if (wave == 0) {
         const size_t gi = (size_t)(tok0 + min(lane, rows - 1)) * HV + hv;
-        if constexpr (kRaw == 0) {
+        if (kRaw == 0 || !in.a) {
             gv = in.g[gi];
             bv = in.beta[gi];
         } else {
@@ -1186,8 +1187,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(
     // SIMD, so the chain keeps its SIMD to itself
 }
 
-// raw: 0 for prepared inputs, 1 / 2 for the fused entry's raw bf16 / fp16
-// inputs (then o has that dtype too).
+// raw: 0 for prepared inputs, 1 / 2 for raw bf16 / fp16 q, k (normalised in
+// the prep; then v and o have that dtype too).
 hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
@@ -1396,4 +1397,28 @@ extern "C" hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k,
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
     return launch_prefill(in, io_dtype == GDN_DTYPE_FP16 ? 2 : 1, o, state, state, nullptr, B, T,
                           B * T, HV, HQK, nc, workspace, workspace_bytes, stream, 0);
+}
+
+// As deltanet_chunk_prefill / _varlen, with q and k rows L2-normalised in the
+// prep kernel (transformers' use_qk_l2norm_in_kernel=True).  cu_seqlens NULL:
+// B sequences of T tokens; else packed, num_seqs sequences of T tokens in
+// total (B must be 1).
+extern "C" hipError_t deltanet_chunk_prefill_l2norm(
+    const void* q, const void* k, const void* v, const float* g, const float* beta, void* o,
+    const float* initial_state, float* final_state, const int32_t* cu_seqlens, int num_seqs,
+    int B, int T, int HV, int HQK, void* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+    if (!dims_ok(HV, HQK, kDK, kDV, kChunk) || B <= 0 || T < 0) return hipErrorInvalidValue;
+    if (cu_seqlens && (B != 1 || num_seqs <= 0)) return hipErrorInvalidValue;
+    if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    PrepIn in = plain_in(q, k, v, g, beta);
+    if (cu_seqlens) {
+        const size_t nc = ((size_t)T + (size_t)(kChunk - 1) * num_seqs) / kChunk;
+        return launch_prefill(in, 1, o, initial_state, final_state, cu_seqlens, num_seqs, 0, T, HV,
+                              HQK, nc, workspace, workspace_bytes, stream, 0);
+    }
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    return launch_prefill(in, 1, o, initial_state, final_state, nullptr, B, T, B * T, HV, HQK, nc,
+                          workspace, workspace_bytes, stream, 0);
 }

@@ -40,7 +40,7 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
                                            const at::Tensor& beta,
                                            const std::optional<at::Tensor>& s0,
                                            const std::optional<at::Tensor>& cu_seqlens,
-                                           bool debug) {
+                                           bool debug, bool qk_l2norm = false) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda(),
                 "all inputs must be CUDA tensors");
     TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
@@ -100,7 +100,13 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
     auto ws = at::empty({(int64_t)ws_bytes}, vc.options().dtype(at::kByte));
 
     hipError_t err;
-    if (cu_seqlens.has_value()) {
+    if (qk_l2norm) {
+        err = deltanet_chunk_prefill_l2norm(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr<float>(), bc.data_ptr<float>(),
+            o.data_ptr(), s0p, sf.data_ptr<float>(),
+            cu_seqlens.has_value() ? cu32.data_ptr<int32_t>() : nullptr, (int)N, (int)B, (int)T,
+            (int)HV, (int)HQK, ws.data_ptr(), ws_bytes, current_stream());
+    } else if (cu_seqlens.has_value()) {
         err = deltanet_chunk_prefill_varlen(
             qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr<float>(), bc.data_ptr<float>(),
             o.data_ptr(), s0p, sf.data_ptr<float>(), cu32.data_ptr<int32_t>(), (int)N, (int)T,
@@ -140,8 +146,8 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
 
 std::vector<at::Tensor> chunk_prefill(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
                                       at::Tensor beta, std::optional<at::Tensor> s0,
-                                      std::optional<at::Tensor> cu_seqlens) {
-    return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/false);
+                                      std::optional<at::Tensor> cu_seqlens, bool qk_l2norm) {
+    return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/false, qk_l2norm);
 }
 
 std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tensor v,
@@ -351,9 +357,10 @@ at::Tensor causal_conv1d_update(const at::Tensor& x, at::Tensor conv_state,
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     using namespace pybind11::literals;
     m.def("chunk_prefill", &chunk_prefill,
-          "chunked gated delta rule prefill (gfx950 HIP); returns [o, final_state]", "q"_a, "k"_a,
-          "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
-          "cu_seqlens"_a = std::nullopt);
+          "chunked gated delta rule prefill (gfx950 HIP); returns [o, final_state]; qk_l2norm: "
+          "q and k rows are raw and L2-normalised in the kernel",
+          "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
+          "cu_seqlens"_a = std::nullopt, "qk_l2norm"_a = false);
     m.def("chunk_prefill_debug", &chunk_prefill_debug,
           "same, also returns per-chunk-head T=(I-A)^-1, A and cumsum(g) views", "q"_a, "k"_a,
           "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),

@@ -8,7 +8,8 @@ The compiled pieces live next to this file:
 
 ``load()`` returns the extension module, whose ops are
 
-  chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None) -> [o, final_state]
+  chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False)
+                                                       -> [o, final_state]
   chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
   recurrent_step(q, k, v, g, beta, state) -> o          (state updated in place)
   chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state) -> o
@@ -51,8 +52,8 @@ def load():
     return _mod
 
 
-def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
-    return load().chunk_prefill(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens)
+def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False):
+    return load().chunk_prefill(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens, qk_l2norm=qk_l2norm)
 
 
 def chunk_prefill_debug(q, k, v, g, beta, s0=None, *, cu_seqlens=None):

@@ -41,6 +41,8 @@ _PROTOS = {
                                      [vp, c_size_t, hipStream_t, vp, c_int]),
     "deltanet_chunk_prefill_kernel": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
                                       [vp, c_size_t, hipStream_t, c_int]),
+    "deltanet_chunk_prefill_l2norm": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, i32p] +
+                                      [c_int] * 5 + [vp, c_size_t, hipStream_t]),
     "deltanet_chunk_prefill_fused": (hipError_t, [vp, vp, vp, vp, vp, fp, vp, vp, fp] +
                                      [c_int] * 5 + [vp, c_size_t, hipStream_t]),
     "gdn_gated_rmsnorm_forward": (hipError_t, [vp, vp, vp, vp, c_int64, c_int, c_float, c_int,

@@ -39,7 +39,10 @@ def _l2norm(x, eps=1e-6):
     return xf * torch.rsqrt((xf * xf).sum(dim=-1, keepdim=True) + eps)
 
 
-def _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel):
+def _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel, kernel_norm=False):
+    """Validate and convert.  With ``kernel_norm`` (the chunked op can
+    normalise bf16 q/k rows itself) and the default scale, bf16 q and k are
+    returned raw and the last element says the kernel must normalise them."""
     import torch
 
     for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
@@ -57,13 +60,16 @@ def _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel):
         raise ValueError("v must be [B, T, HV, 128] with HV a multiple of the q/k heads")
     if g.shape != (B, T, HV) or beta.shape != (B, T, HV):
         raise ValueError("g and beta must be [B, T, HV]")
-    if use_qk_l2norm_in_kernel:
-        q, k = _l2norm(q), _l2norm(k)
-    if scale is not None and abs(float(scale) - _KERNEL_SCALE) > 1e-12:
-        q = q.float() * (float(scale) / _KERNEL_SCALE)   # the kernels scale q by 1/sqrt(128)
+    custom_scale = scale is not None and abs(float(scale) - _KERNEL_SCALE) > 1e-12
     bf = torch.bfloat16
+    in_kernel = (use_qk_l2norm_in_kernel and kernel_norm and not custom_scale
+                 and q.dtype == bf and k.dtype == bf)
+    if use_qk_l2norm_in_kernel and not in_kernel:
+        q, k = _l2norm(q), _l2norm(k)
+    if custom_scale:
+        q = q.float() * (float(scale) / _KERNEL_SCALE)   # the kernels scale q by 1/sqrt(128)
     return (q.to(bf).contiguous(), k.to(bf).contiguous(), v.to(bf).contiguous(),
-            g.float().contiguous(), beta.float().contiguous(), HV)
+            g.float().contiguous(), beta.float().contiguous(), HV, in_kernel)
 
 
 def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
@@ -73,7 +79,8 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     final_state None unless ``output_final_state``."""
     import torch
 
-    q, k, v, g, beta, HV = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel)
+    q, k, v, g, beta, HV, norm = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel,
+                                          kernel_norm=True)
     s0 = None
     if initial_state is not None:
         s0 = initial_state.float().contiguous()
@@ -81,9 +88,10 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
         if q.shape[0] != 1:
             raise ValueError("with cu_seqlens the batch must be one packed row (B = 1)")
         o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0,
-                                      cu_seqlens=cu_seqlens.to(torch.int32).contiguous())
+                                      cu_seqlens=cu_seqlens.to(torch.int32).contiguous(),
+                                      qk_l2norm=norm)
     else:
-        o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0)
+        o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0, qk_l2norm=norm)
     return o, (sf if output_final_state else None)
 
 
@@ -96,7 +104,7 @@ def recurrent_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
 
     if cu_seqlens is not None:
         raise NotImplementedError("recurrent_gated_delta_rule takes no cu_seqlens here")
-    q, k, v, g, beta, HV = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel)
+    q, k, v, g, beta, HV, _ = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel)
     B = q.shape[0]
     if initial_state is None:
         state = torch.zeros(B, HV, _D, _D, dtype=torch.float32, device=q.device)

@@ -144,6 +144,25 @@ def test_fused_prefill_rejects_on_host(lib):
     assert c(a9=0) == INVALID
 
 
+def test_l2norm_prefill_rejects_on_host(lib):
+    f = lib.deltanet_chunk_prefill_l2norm
+    # q, k, v, g, beta, o, s0, sf, cu, num_seqs, B, T, HV, HQK, ws, ws bytes, stream
+    ok = [1, 1, 1, 1, 1, 1, None, 1, None, 0, 1, 64, 4, 2, 1, 1 << 40, None]
+
+    def c(**over):
+        a = list(ok)
+        for i, v in over.items():
+            a[int(i[1:])] = v
+        return f(*a)
+
+    assert c(a13=3) == INVALID                               # HV % HQK
+    assert c(a8=1, a9=2, a10=2) == INVALID                   # packed needs B = 1
+    assert c(a8=1, a9=0) == INVALID                          # packed needs num_seqs > 0
+    assert c(a7=None) == INVALID and c(a14=None) == INVALID
+    assert c(a0=None) == INVALID and c(a3=None) == INVALID
+    assert c(a15=16) == INVALID                              # short workspace
+
+
 def test_conv_reject_on_host(lib):
     fwd = lib.gdn_causal_conv1d_fwd
     bf, fp32 = capi.DTYPE_BF16, capi.DTYPE_FP32

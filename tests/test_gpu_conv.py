@@ -115,6 +115,28 @@ def test_update_matches_oracle(ops, dev, B, T, L):
     assert torch.equal(st_d.cpu(), ref_st)
 
 
+@pytest.mark.parametrize("io,wd", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                   (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("T", [1, 3])
+def test_update_vector_path_dtypes_and_bias(ops, dev, io, wd, T):
+    """The 4-channel update path (K = 4, 4-token state rows) with every
+    weight dtype, a bias and B > 1, against the oracle."""
+    gen = torch.Generator().manual_seed(7 + T)
+    B, D = 3, 1024
+    x = torch.randn(B, T, D, generator=gen).to(io).transpose(1, 2)
+    st = torch.randn(B, D, 4, generator=gen).to(io)
+    w = (0.5 * torch.randn(D, 4, generator=gen)).to(wd)
+    bias = (0.1 * torch.randn(D, generator=gen)).to(wd)
+    for act in (None, "silu"):
+        ref, ref_st = orc.causal_conv1d_update(x, st, w, bias, act)
+        print(f"update4 B={B} T={T} D={D} {io} w={wd} act={act}", flush=True)
+        st_d = st.to(dev)
+        y = ops.causal_conv1d_update(x.to(dev), st_d, w.to(dev), bias.to(dev), act is not None)
+        torch.cuda.synchronize()
+        _check(y, ref, act, f"update4 {io} {wd} {act} T={T}")
+        assert torch.equal(st_d.cpu(), ref_st)
+
+
 def test_prefill_then_decode_chain(ops, dev):
     """Prefill 40 tokens, then 6 single-token updates from the state the
     prefill leaves: the outputs equal one pass over all 46 tokens."""

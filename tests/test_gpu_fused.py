@@ -45,6 +45,11 @@ def test_fused_small(ops, dev, dtype, T):
            tag=f"{dtype} B2 T{T}", ref_bar=T > 1)
 
 
+def test_fused_batch_gqa(ops, dev):
+    """B=2 with the plugin's head layout (HK=16, HV=32) and a ragged tail."""
+    _fused(ops, dev, *gc.fused_inputs(24, B=2, T=200, HK=16, HV=32), tag="fp16 B2 T200 HV32")
+
+
 def test_fused_empty_sequence_keeps_state(ops, dev):
     q, k, v, a, b, A_log, dt_bias, s0 = gc.fused_inputs(22, B=1, T=0, HK=2, HV=4)
     st = s0.to(dev).contiguous()
@@ -71,5 +76,33 @@ def test_fused_matches_unfused_path(ops, dev):
     same = (o_f == o_u16).float().mean().item()
     do = (o_f.float() - o_u16.float()).abs().max().item()
     ds = (st - s_u).abs().max().item()
+    print(f"    o identical {same * 100:.3f}%  max|do|={do:.3e}  max|dS|={ds:.3e}", flush=True)
+    assert same > 0.99 and do < 1e-2 and ds < 1e-3
+
+
+@pytest.mark.parametrize("varlen", [False, True])
+def test_in_kernel_l2norm_matches_normalised_inputs(ops, dev, varlen):
+    """chunk_prefill(..., qk_l2norm=True) on raw bf16 q/k == chunk_prefill on
+    rows normalised by torch (fp32, eps 1e-6, rounded to bf16), up to the
+    last bits of the norm (a bf16 rounding of a q or k element can flip)."""
+    gen = torch.Generator().manual_seed(31)
+    T, HK, HV = 300, 4, 8
+    q = torch.randn(1, T, HK, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(1, T, HK, 128, generator=gen).to(torch.bfloat16)
+    _, _, v, g, beta, s0 = gc.make_gdn_inputs(32, B=1, T=T, HK=HK, HV=HV)
+    cu = torch.tensor([0, 120, 121, 300], dtype=torch.int32) if varlen else None
+    if varlen:
+        s0 = 0.02 * torch.randn(3, HV, 128, 128, generator=gen)
+    d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
+    kw = {"cu_seqlens": cu.to(dev)} if varlen else {}
+    print(f"[l2norm] in-kernel vs torch-normalised, T{T} HK{HK} HV{HV} varlen={varlen}", flush=True)
+    o_k, s_k = ops.chunk_prefill(*d, qk_l2norm=True, **kw)
+    qn = orc.l2norm(d[0].float()).to(torch.bfloat16)
+    kn = orc.l2norm(d[1].float()).to(torch.bfloat16)
+    o_t, s_t = ops.chunk_prefill(qn, kn, *d[2:], **kw)
+    torch.cuda.synchronize()
+    same = (o_k == o_t).float().mean().item()
+    do = (o_k.float() - o_t.float()).abs().max().item()
+    ds = (s_k - s_t).abs().max().item()
     print(f"    o identical {same * 100:.3f}%  max|do|={do:.3e}  max|dS|={ds:.3e}", flush=True)
     assert same > 0.99 and do < 1e-2 and ds < 1e-3
