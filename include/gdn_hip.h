@@ -156,6 +156,14 @@ hipError_t deltanet_recurrent_step(const void* q, const void* k, const void* v, 
                                    const float* beta, void* o, float* state, int B, int T, int HV,
                                    int HQK, int DK, int DV, hipStream_t stream);
 
+/* deltanet_recurrent_step with raw bf16 q and k rows, L2-normalised in the
+ * kernel as in deltanet_chunk_prefill_l2norm (transformers'
+ * use_qk_l2norm_in_kernel=True for decode, modeling_qwen3_5.py:343-345). */
+hipError_t deltanet_recurrent_step_l2norm(const void* q, const void* k, const void* v,
+                                          const float* g, const float* beta, void* o,
+                                          float* state, int B, int T, int HV, int HQK, int DK,
+                                          int DV, hipStream_t stream);
+
 /* Gated RMSNorm y = rmsnorm(x) * w * silu(z) over rows of dv elements.
  * Replaces kernel::gatedRmsNormForward (export/patches/orin_text_engine/files/
  * cpp/kernels/gatedRmsNorm/gatedRmsNormKernel.h:17-18), which was fp16-only.

@@ -27,6 +27,9 @@ namespace {
 constexpr int kDecThreads = 256;
 constexpr int kRowsPerThread = kDK / 8;  // 16
 
+// kNorm: q and k rows are raw and normalised here first, x rsqrt(sum x^2 +
+// 1e-6) in fp32 rounded to bf16 (transformers' use_qk_l2norm_in_kernel).
+template <bool kNorm>
 __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ g,
@@ -60,6 +63,23 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
         const float gt = g[tk * HV + hv];
         const float bt = beta[tk * HV + hv];
         __syncthreads();
+        if (kNorm) {
+            if (wave == 0) {
+                const int l = tid;
+                float pq = qs[l] * qs[l] + qs[l + 64] * qs[l + 64];
+                float pk = ks[l] * ks[l] + ks[l + 64] * ks[l + 64];
+                for (int off = 32; off > 0; off >>= 1) {
+                    pq += __shfl_xor(pq, off, 64);
+                    pk += __shfl_xor(pk, off, 64);
+                }
+                const float iq = rsqrtf(pq + 1e-6f), ik = rsqrtf(pk + 1e-6f);
+                qs[l] = bf16_bits_to_f32(f32_to_bf16_bits(qs[l] * iq));
+                qs[l + 64] = bf16_bits_to_f32(f32_to_bf16_bits(qs[l + 64] * iq));
+                ks[l] = bf16_bits_to_f32(f32_to_bf16_bits(ks[l] * ik));
+                ks[l + 64] = bf16_bits_to_f32(f32_to_bf16_bits(ks[l + 64] * ik));
+            }
+            __syncthreads();
+        }
         if (wave == 0) {
             float p = qs[tid] * ks[tid] + qs[tid + 64] * ks[tid + 64];
             for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off, 64);
@@ -115,18 +135,35 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
 
 using namespace gdn;
 
-extern "C" hipError_t deltanet_recurrent_step(const void* q, const void* k, const void* v,
-                                              const float* g, const float* beta, void* o,
-                                              float* state, int B, int T, int HV, int HQK,
-                                              int DK, int DV, hipStream_t stream) {
+namespace {
+hipError_t recurrent_launch(const void* q, const void* k, const void* v, const float* g,
+                            const float* beta, void* o, float* state, int B, int T, int HV,
+                            int HQK, int DK, int DV, hipStream_t stream, bool norm) {
     if (DK != kDK || DV != kDV || B <= 0 || T < 0 || HV <= 0 || HQK <= 0 || HV % HQK != 0)
         return hipErrorInvalidValue;
     if (!state) return hipErrorInvalidValue;
     if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
-    hipLaunchKernelGGL(gdn_recurrent_kernel, dim3((unsigned)(B * HV)), dim3(kDecThreads), 0, stream,
+    hipLaunchKernelGGL(norm ? gdn_recurrent_kernel<true> : gdn_recurrent_kernel<false>,
+                       dim3((unsigned)(B * HV)), dim3(kDecThreads), 0, stream,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), g, beta, static_cast<uint16_t*>(o), state,
                        T, HV, HQK, 1.0f / sqrtf((float)kDK));
     return hipGetLastError();
+}
+}  // namespace
+
+extern "C" hipError_t deltanet_recurrent_step(const void* q, const void* k, const void* v,
+                                              const float* g, const float* beta, void* o,
+                                              float* state, int B, int T, int HV, int HQK,
+                                              int DK, int DV, hipStream_t stream) {
+    return recurrent_launch(q, k, v, g, beta, o, state, B, T, HV, HQK, DK, DV, stream, false);
+}
+
+extern "C" hipError_t deltanet_recurrent_step_l2norm(const void* q, const void* k, const void* v,
+                                                     const float* g, const float* beta, void* o,
+                                                     float* state, int B, int T, int HV,
+                                                     int HQK, int DK, int DV,
+                                                     hipStream_t stream) {
+    return recurrent_launch(q, k, v, g, beta, o, state, B, T, HV, HQK, DK, DV, stream, true);
 }

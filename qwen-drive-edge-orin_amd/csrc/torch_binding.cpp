@@ -158,7 +158,7 @@ std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tens
 }
 
 at::Tensor recurrent_step(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
-                          at::Tensor beta, at::Tensor state) {
+                          at::Tensor beta, at::Tensor state, bool qk_l2norm) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda() &&
                     state.is_cuda(),
                 "all inputs must be CUDA tensors");
@@ -189,10 +189,10 @@ at::Tensor recurrent_step(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g
                     state.size(3) == DV,
                 "state must be [B, HV, DK, DV]");
     auto o = at::empty_like(vc);
-    check_hip(deltanet_recurrent_step(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                      gc.data_ptr<float>(), bc.data_ptr<float>(), o.data_ptr(),
-                                      state.data_ptr<float>(), (int)B, (int)T, (int)HV, (int)HQK,
-                                      (int)DK, (int)DV, current_stream()),
+    auto step = qk_l2norm ? deltanet_recurrent_step_l2norm : deltanet_recurrent_step;
+    check_hip(step(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr<float>(),
+                   bc.data_ptr<float>(), o.data_ptr(), state.data_ptr<float>(), (int)B, (int)T,
+                   (int)HV, (int)HQK, (int)DK, (int)DV, current_stream()),
               "deltanet_recurrent_step");
     return o;
 }
@@ -367,7 +367,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "cu_seqlens"_a = std::nullopt);
     m.def("recurrent_step", &recurrent_step,
           "recurrent gated delta rule (decode), state updated in place; returns o", "q"_a, "k"_a,
-          "v"_a, "g"_a, "beta"_a, "state"_a);
+          "v"_a, "g"_a, "beta"_a, "state"_a, pybind11::kw_only(), "qk_l2norm"_a = false);
     m.def("chunk_prefill_fused", &chunk_prefill_fused,
           "prefill on raw inputs (q/k L2 norm, gates, dtype conversions fused); state updated "
           "in place; returns o",

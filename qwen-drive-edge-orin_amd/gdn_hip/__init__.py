@@ -11,7 +11,8 @@ The compiled pieces live next to this file:
   chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False)
                                                        -> [o, final_state]
   chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
-  recurrent_step(q, k, v, g, beta, state) -> o          (state updated in place)
+  recurrent_step(q, k, v, g, beta, state, *, qk_l2norm=False) -> o
+                                                        (state updated in place)
   chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state) -> o
                           raw q/k/v and gate inputs     (state updated in place)
   gated_rmsnorm(x, z, weight, eps=1e-6) -> y
@@ -64,8 +65,8 @@ def chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state):
     return load().chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state)
 
 
-def recurrent_step(q, k, v, g, beta, state):
-    return load().recurrent_step(q, k, v, g, beta, state)
+def recurrent_step(q, k, v, g, beta, state, *, qk_l2norm=False):
+    return load().recurrent_step(q, k, v, g, beta, state, qk_l2norm=qk_l2norm)
 
 
 def gated_rmsnorm(x, z, weight, eps=1e-6):

@@ -35,6 +35,8 @@ _PROTOS = {
                                       [c_int] * 7 + [vp, c_size_t, hipStream_t, c_int]),
     "deltanet_recurrent_step": (hipError_t, [vp, vp, vp, fp, fp, vp, fp] + [c_int] * 6 +
                                 [hipStream_t]),
+    "deltanet_recurrent_step_l2norm": (hipError_t, [vp, vp, vp, fp, fp, vp, fp] + [c_int] * 6 +
+                                       [hipStream_t]),
     "deltanet_prefill_kernel_count": (c_int, []),
     "deltanet_prefill_kernel_name": (ct.c_char_p, [c_int]),
     "deltanet_chunk_prefill_timed": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +

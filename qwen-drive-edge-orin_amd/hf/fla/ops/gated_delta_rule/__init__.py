@@ -40,8 +40,8 @@ def _l2norm(x, eps=1e-6):
 
 
 def _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel, kernel_norm=False):
-    """Validate and convert.  With ``kernel_norm`` (the chunked op can
-    normalise bf16 q/k rows itself) and the default scale, bf16 q and k are
+    """Validate and convert.  With ``kernel_norm`` (the kernels can normalise
+    bf16 q/k rows themselves) and the default scale, bf16 q and k are
     returned raw and the last element says the kernel must normalise them."""
     import torch
 
@@ -104,11 +104,12 @@ def recurrent_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
 
     if cu_seqlens is not None:
         raise NotImplementedError("recurrent_gated_delta_rule takes no cu_seqlens here")
-    q, k, v, g, beta, HV, _ = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel)
+    q, k, v, g, beta, HV, norm = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel,
+                                          kernel_norm=True)
     B = q.shape[0]
     if initial_state is None:
         state = torch.zeros(B, HV, _D, _D, dtype=torch.float32, device=q.device)
     else:
         state = initial_state.float().clone().contiguous()
-    o = gdn_hip.recurrent_step(q, k, v, g, beta, state)
+    o = gdn_hip.recurrent_step(q, k, v, g, beta, state, qk_l2norm=norm)
     return o, (state if output_final_state else None)

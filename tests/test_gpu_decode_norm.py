@@ -85,3 +85,27 @@ def test_rmsnorm_variants(ops, dev, dtype, wdt, dv):
     w = 1 + 0.1 * torch.randn(dv, generator=gen)
     w = w.to(dtype) if wdt == "io" else w
     _norm_check(ops, dev, x, z, w, 1e-6, tag=f"{dtype} w={wdt} dv={dv}")
+
+
+def test_decode_in_kernel_l2norm_matches_normalised_inputs(ops, dev):
+    """recurrent_step(..., qk_l2norm=True) on raw bf16 q/k == recurrent_step
+    on rows normalised by torch (fp32, eps 1e-6, rounded to bf16), up to the
+    last bits of the norm."""
+    gen = torch.Generator().manual_seed(41)
+    B, T, HK, HV = 4, 3, 2, 4
+    q = torch.randn(B, T, HK, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(B, T, HK, 128, generator=gen).to(torch.bfloat16)
+    _, _, v, g, beta, s0 = gc.make_gdn_inputs(42, B=B, T=T, HK=HK, HV=HV)
+    d = [t.to(dev) for t in (q, k, v, g, beta)]
+    print(f"[decode] in-kernel l2norm B{B} T{T} HK{HK} HV{HV}", flush=True)
+    st_k, st_t = s0.to(dev), s0.to(dev)
+    o_k = ops.recurrent_step(*d, st_k, qk_l2norm=True)
+    qn = orc.l2norm(d[0].float()).to(torch.bfloat16)
+    kn = orc.l2norm(d[1].float()).to(torch.bfloat16)
+    o_t = ops.recurrent_step(qn, kn, *d[2:], st_t)
+    torch.cuda.synchronize()
+    same = (o_k == o_t).float().mean().item()
+    do = (o_k.float() - o_t.float()).abs().max().item()
+    ds = (st_k - st_t).abs().max().item()
+    print(f"    o identical {same * 100:.3f}%  max|do|={do:.3e}  max|dS|={ds:.3e}", flush=True)
+    assert same > 0.99 and do < 1e-2 and ds < 1e-3
