@@ -367,7 +367,8 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
         }
     }
     // this wave's Q rows (k-map over dk); bf16 straight into the MFMA.
-    // They are needed right after K, V only at the end: Q is loaded first
+    // They are needed right after K (V, needed only at the end, is loaded
+    // later)
     uint2 qr[4][2];
     {
         const uint16_t* qs =
@@ -378,23 +379,9 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
             qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
         }
     }
-    // this wave's V rows for value columns 32 w .. 32 w + 31 (the U slices
-    // 2w, 2w+1), k-mapped like an A operand: token tile tt, row 16 tt + lm
-    uint2 vr[4][2];
-    {
-        const uint16_t* vs = v + (size_t)hv * kDV + 32 * wave + 4 * lg;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const uint16_t* vrow = vs + (size_t)(tok0 + min(16 * tt + lm, rows - 1)) * HV * kDV;
-            vr[tt][0] = *reinterpret_cast<const uint2*>(vrow);
-            vr[tt][1] = *reinterpret_cast<const uint2*>(vrow + 16);
-        }
-    }
-
     if constexpr (kRaw != 0) {
         // raw inputs: K rows (16 lanes per row, 8 values each) and Q rows (4
-        // lanes per row, 32 values each) L2-normalised and rounded to bf16;
-        // fp16 V rounded to bf16
+        // lanes per row, 32 values each) L2-normalised and rounded to bf16
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
             float ss = 0.f;
@@ -425,16 +412,6 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
                 for (int h2 = 0; h2 < 2; ++h2) {
                     qr[kb][h2].x = norm_pair<kRaw>(qr[kb][h2].x, inv);
                     qr[kb][h2].y = norm_pair<kRaw>(qr[kb][h2].y, inv);
-                }
-            }
-        }
-        if constexpr (kRaw == 2) {
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
-                    vr[tt][h2].x = norm_pair<kRaw>(vr[tt][h2].x, 1.0f);
-                    vr[tt][h2].y = norm_pair<kRaw>(vr[tt][h2].y, 1.0f);
                 }
             }
         }
@@ -589,6 +566,21 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     }
     __syncthreads();
 
+    // this wave's V rows for value columns 32 w .. 32 w + 31 (the U slices
+    // 2w, 2w+1), k-mapped like an A operand: token tile tt, row 16 tt + lm.
+    // Issued here, a whole inverse ahead of their use, so they stay out of
+    // the burst of K, Q and gate loads every group starts with.
+    uint2 vr[4][2];
+    {
+        const uint16_t* vs = v + (size_t)hv * kDV + 32 * wave + 4 * lg;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const uint16_t* vrow = vs + (size_t)(tok0 + min(16 * tt + lm, rows - 1)) * HV * kDV;
+            vr[tt][0] = *reinterpret_cast<const uint2*>(vrow);
+            vr[tt][1] = *reinterpret_cast<const uint2*>(vrow + 16);
+        }
+    }
+
     // ---- T = (I - A)^-1 in fp32, in place in AT
     // (1) 16x16 diagonal blocks by forward substitution: wave 0, lane =
     //     16 * block + column; T[i][c] = sum_{j<i} A[i][j] T[j][c] for i > c,
@@ -691,6 +683,17 @@ __global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
     // ---- U = (T diag(beta)) V: slices nt = 2w, 2w+1, all four row tiles.
     // T is lower triangular: row tiles 0 and 1 see only tokens 0..31.
     {
+        if constexpr (kRaw == 2) {
+            // raw fp16 V rounded to bf16
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    vr[tt][h2].x = norm_pair<kRaw>(vr[tt][h2].x, 1.0f);
+                    vr[tt][h2].y = norm_pair<kRaw>(vr[tt][h2].y, 1.0f);
+                }
+            }
+        }
         bf16x8 vrf[4];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) vrf[tt] = bf16_frag(vr[tt][0], vr[tt][1]);
