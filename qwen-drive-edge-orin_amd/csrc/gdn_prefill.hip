@@ -312,7 +312,7 @@ __device__ inline void am_products(const bf16x8 (&ka)[4][4], const bf16x8 (&qf)[
 }
 
 template <bool kDbg, int kRaw>
-__global__ __launch_bounds__(kPrepThreads, 3) void gdn_prep_kernel(
+__global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     PrepIn in, const int32_t* __restrict__ cu, int N, int T, int HV, int HK, int nch_bound,
     float scale, Workspace ws) {
     __shared__ PrepSmem sm;
