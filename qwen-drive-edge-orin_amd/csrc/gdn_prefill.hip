@@ -40,6 +40,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace gdn {
 namespace {
 
@@ -1274,7 +1276,9 @@ extern "C" size_t deltanet_prefill_workspace_size(int B, int T, int HV, int DK, 
                                                   int chunk_size) {
     if (B <= 0 || T < 0 || HV <= 0 || DK != kDK || DV != kDV || chunk_size != kChunk) return 0;
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
-    return WsLayout(nc * HV).total;
+    // at least one 256-byte block, so T = 0 (no chunks) still gets a valid
+    // nonzero size and 0 keeps meaning "unsupported"
+    return std::max<size_t>(WsLayout(nc * HV).total, 256);
 }
 
 extern "C" hipError_t deltanet_chunk_prefill(const void* q, const void* k, const void* v,
@@ -1341,7 +1345,7 @@ extern "C" size_t deltanet_prefill_varlen_workspace_size(int total_tokens, int n
         return 0;
     // sum_i ceil(L_i / C) <= (sum_i L_i + (C-1) N) / C
     const size_t nc = ((size_t)total_tokens + (size_t)(kChunk - 1) * num_seqs) / kChunk;
-    return WsLayout(nc * HV).total;
+    return std::max<size_t>(WsLayout(nc * HV).total, 256);
 }
 
 extern "C" hipError_t deltanet_chunk_prefill_varlen(

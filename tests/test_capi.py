@@ -35,6 +35,7 @@ def test_workspace_size(lib):
     assert ws(1, 1141, 32, 128, 64, 64) == 0          # DV != 128
     assert ws(1, 1141, 32, 128, 128, 32) == 0         # chunk != 64
     assert ws(0, 10, 32, 128, 128, 64) == 0
+    assert ws(1, 0, 32, 128, 128, 64) > 0              # T = 0: no chunks, still a valid size
     # grows with chunks and heads; tcop twin is the same size
     assert ws(1, 1152, 32, 128, 128, 64) == ws(1, 1141, 32, 128, 128, 64)
     assert ws(1, 1153, 32, 128, 128, 64) > ws(1, 1152, 32, 128, 128, 64)
@@ -48,6 +49,7 @@ def test_workspace_size(lib):
     assert vws(sum(lens), 8, 32, 128, 128, 64) >= ws(1, 64 * chunks, 32, 128, 128, 64)
     assert vws(8 * 65, 8, 32, 128, 128, 64) >= ws(1, 64 * 16, 32, 128, 128, 64)
     assert vws(100, 0, 32, 128, 128, 64) == 0
+    assert vws(0, 1, 32, 128, 128, 64) > 0
 
 
 def _prefill_args(**over):

@@ -117,6 +117,35 @@ def test_varlen_equals_per_sequence_calls(ops, dev):
         assert torch.equal(si[0], sf[i]), f"seq {i} state"
 
 
+def test_empty_sequence(ops, dev):
+    """T = 0: o is empty and the final state is the initial one (zeros without one)."""
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.make_gdn_inputs(9, B=2, T=0, HK=2, HV=4)]
+    s0 = torch.randn(2, 4, 128, 128, device=dev)
+    o, sf = ops.chunk_prefill(q, k, v, g, beta, s0)
+    assert o.shape == (2, 0, 4, 128) and torch.equal(sf, s0)
+    _, sf0 = ops.chunk_prefill(q, k, v, g, beta, None)
+    assert torch.count_nonzero(sf0).item() == 0
+
+
+@pytest.mark.parametrize("n", [64, 65, 100])
+def test_varlen_many_sequences(ops, dev, n):
+    """More sequences than the scan's longest-first ordering table holds (64):
+    the packed call is still bitwise the per-sequence calls, lengths 0..100."""
+    gen = torch.Generator().manual_seed(700 + n)
+    lens = torch.randint(0, 101, (n,), generator=gen)
+    lens[n // 3] = 0
+    q, k, v, g, beta, s0, cu = gc.varlen_inputs(lens)
+    print(f"[varlen-many] n={n} tokens={int(lens.sum())}", flush=True)
+    d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
+    o, sf = ops.chunk_prefill(*d, cu_seqlens=cu.to(dev))
+    for i in range(n):
+        a, b = int(cu[i]), int(cu[i + 1])
+        oi, si = ops.chunk_prefill(d[0][:, a:b], d[1][:, a:b], d[2][:, a:b], d[3][:, a:b],
+                                   d[4][:, a:b], d[5][i:i + 1])
+        assert torch.equal(oi, o[:, a:b]), f"seq {i} o"
+        assert torch.equal(si[0], sf[i]), f"seq {i} state"
+
+
 def test_gqa_equals_expanded_heads(ops, dev):
     """HK=16 -> HV=32 sharing is bitwise the explicit repeat_interleave."""
     q, k, v, g, beta, s0 = [t.to(dev) for t in gc.prefill_inputs()]
