@@ -149,19 +149,11 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
     const int d0 = (ct * kConvThreads + threadIdx.x) * 8;
     if (d0 >= D) return;
     const int len = min(run, T - t0);   // >= 1: the launcher makes n_runs = ceil(T / run)
+    __builtin_assume(len >= 1);         // the first output is unconditional
     const uint16_t* xb = x + (size_t)b * xbs + d0;
     uint16_t* yb = y + (size_t)b * ybs + d0;
-    // all loads first: rows t0-K+1 .. t0+len-1; rows before 0 are zero, the
-    // slots past the run re-read its last row (a cache hit) and stay unused
-    constexpr int kRows = kConvMaxRun + K - 1;
-    u32x4 raw[kRows];
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-        const int t = t0 - (K - 1) + i;
-        const int tc = min(max(t, 0), t0 + len - 1);
-        raw[i] = *reinterpret_cast<const u32x4*>(xb + (size_t)tc * xts);   // cached: halo rows
-        if (t < 0) raw[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+    // weights (and bias) first: loads complete in issue order, so the first
+    // outputs can then start as soon as their own rows arrive
     float wf[8][K], bf[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -169,6 +161,21 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
         for (int j = 0; j < K; ++j) wf[e][j] = ld_elem<WT>(w, (size_t)(d0 + e) * K + j);
         if constexpr (BIAS) bf[e] = ld_elem<WT>(bias, d0 + e);
     }
+    // then all rows t0-K+1 .. t0+len-1; rows before 0 are zero, the slots
+    // past the run re-read its last row (a cache hit)
+    constexpr int kRows = kConvMaxRun + K - 1;
+    u32x4 raw[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+        const int tc = min(max(t0 - (K - 1) + i, 0), t0 + len - 1);
+        raw[i] = *reinterpret_cast<const u32x4*>(xb + (size_t)tc * xts);   // cached: halo rows
+    }
+    // every load is issued before any is waited for: the scheduler would
+    // otherwise hold back later rows behind the first rows' use
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i)
+        if (t0 - (K - 1) + i < 0) raw[i] = u32x4{0u, 0u, 0u, 0u};
     // sliding window of K unpacked rows: win[j] = row i + j
     float win[K][8];
 #pragma unroll
@@ -179,27 +186,30 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
             win[j][2 * p + 1] = hi16<IO>(raw[j][p]);
         }
     }
+    // Rows are unpacked outside the `i < len` guards, and the first output
+    // is unconditional: a row read inside one guarded block only lets the
+    // compiler sink its load into that block, where it is issued late and
+    // waited for at once.
 #pragma unroll
     for (int i = 0; i < kConvMaxRun; ++i) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            win[K - 1][2 * p] = lo16<IO>(raw[i + K - 1][p]);
+            win[K - 1][2 * p + 1] = hi16<IO>(raw[i + K - 1][p]);
+        }
         if (i < len) {   // uniform over the work-group
+        float acc[8];
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                win[K - 1][2 * p] = lo16<IO>(raw[i + K - 1][p]);
-                win[K - 1][2 * p + 1] = hi16<IO>(raw[i + K - 1][p]);
-            }
-            float acc[8];
+        for (int e = 0; e < 8; ++e) {
+            // +0 start: an all-zero window gives +0, as a sum from zero
+            float a = fmaf(wf[e][0], win[0][e], 0.0f);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                // +0 start: an all-zero window gives +0, as a sum from zero
-                float a = fmaf(wf[e][0], win[0][e], 0.0f);
-#pragma unroll
-                for (int j = 1; j < K; ++j) a = fmaf(wf[e][j], win[j][e], a);
-                if constexpr (BIAS) a += bf[e];
-                acc[e] = a;
-            }
-            const u32x4 out = finish8<IO, WT, SILU>(acc);
-            __builtin_nontemporal_store(out,
-                                        reinterpret_cast<u32x4*>(yb + (size_t)(t0 + i) * yts));
+            for (int j = 1; j < K; ++j) a = fmaf(wf[e][j], win[j][e], a);
+            if constexpr (BIAS) a += bf[e];
+            acc[e] = a;
+        }
+        const u32x4 out = finish8<IO, WT, SILU>(acc);
+        __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(yb + (size_t)(t0 + i) * yts));
         }
 #pragma unroll
         for (int j = 0; j < K - 1; ++j) {
