@@ -53,13 +53,22 @@ __global__ __launch_bounds__(kNormThreads) void gated_rmsnorm_kernel(
     const int64_t row = ((int64_t)blockIdx.x * kNormThreads + threadIdx.x) / LPR;
     const int sub = threadIdx.x % LPR;
     const bool active = row < rows;
-    const int64_t off = row * dv + sub * 8;
+    // threads past the last row (last block only) read that row again and
+    // store nothing, so every load is unconditional: weights first, then the
+    // row of x and of z
+    const int64_t off = (active ? row : rows - 1) * dv + sub * 8;
 
-    u32x4 xr = {0u, 0u, 0u, 0u}, zr = {0u, 0u, 0u, 0u};
-    if (active) {
-        xr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + off));
-        zr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(z + off));
+    f32x4 w0, w1;
+    u32x4 wr;
+    if (W == 2) {
+        const f32x4* wp = reinterpret_cast<const f32x4*>(static_cast<const float*>(w) + sub * 8);
+        w0 = wp[0];
+        w1 = wp[1];
+    } else {
+        wr = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w) + sub * 8);
     }
+    const u32x4 xr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + off));
+    const u32x4 zr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(z + off));
     const uint32_t xw[4] = {xr[0], xr[1], xr[2], xr[3]};
     const uint32_t zw[4] = {zr[0], zr[1], zr[2], zr[3]};
     float xf[8], zf[8];
@@ -79,15 +88,12 @@ __global__ __launch_bounds__(kNormThreads) void gated_rmsnorm_kernel(
 
     float wf[8];
     if (W == 2) {
-        const f32x4* wp = reinterpret_cast<const f32x4*>(static_cast<const float*>(w) + sub * 8);
-        const f32x4 w0 = wp[0], w1 = wp[1];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             wf[j] = w0[j];
             wf[4 + j] = w1[j];
         }
     } else {
-        const u32x4 wr = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w) + sub * 8);
         const uint32_t ww[4] = {wr[0], wr[1], wr[2], wr[3]};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -113,6 +119,10 @@ __global__ __launch_bounds__(kNormThreads) void gated_rmsnorm_kernel(
         }
         out[p] = pk;
     }
+    // the outputs are formed before the store's guard: otherwise the
+    // compiler moves their whole computation, z and w loads included, into
+    // the guarded block, behind the wait for x
+    asm volatile("" ::"v"(out[0]), "v"(out[1]), "v"(out[2]), "v"(out[3]));
     if (active) {
         const u32x4 o4 = {out[0], out[1], out[2], out[3]};
         __builtin_nontemporal_store(o4, reinterpret_cast<u32x4*>(y + off));
