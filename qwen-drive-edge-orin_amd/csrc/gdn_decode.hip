@@ -47,6 +47,26 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
     const int b = bh / HV, hv = bh - b * HV;
     const int hk = hv / (HV / HK);
 
+    // A token's inputs: this thread's element of q (threads 0..127) or k
+    // (128..255), its four v columns, g and beta.  Token 0's are requested
+    // before the state, so forming q and k needs only them; each later
+    // token's are requested during the previous token's work.
+    const uint16_t* qk = tid < kDK ? q + (size_t)hk * kDK + tid : k + (size_t)hk * kDK + tid - kDK;
+    float* qk_dst = tid < kDK ? qs + tid : ks + tid - kDK;
+    auto load_token = [&](int t, uint16_t& qkr, uint2& vr, float& gr, float& br) {
+        const size_t tk = (size_t)b * T + t;
+        qkr = qk[tk * HK * kDK];
+        vr = *reinterpret_cast<const uint2*>(v + (tk * HV + hv) * kDV + 4 * cb);
+        gr = g[tk * HV + hv];
+        br = beta[tk * HV + hv];
+    };
+    uint16_t qkr;
+    uint2 vraw;
+    float gt, bt;
+    __builtin_assume(T >= 1);   // the launcher returns before T = 0
+    load_token(0, qkr, vraw, gt, bt);
+    __builtin_amdgcn_sched_barrier(0);   // keeps them ahead of the state loads
+
     float* S = state + (size_t)bh * kDK * kDV;
     f32x4 s[kRowsPerThread];
 #pragma unroll
@@ -55,13 +75,7 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
 
     for (int t = 0; t < T; ++t) {
         const size_t tk = ((size_t)b * T + t);
-        if (tid < kDK) {
-            qs[tid] = bf16_bits_to_f32(q[(tk * HK + hk) * kDK + tid]);
-        } else {
-            ks[tid - kDK] = bf16_bits_to_f32(k[(tk * HK + hk) * kDK + tid - kDK]);
-        }
-        const float gt = g[tk * HV + hv];
-        const float bt = beta[tk * HV + hv];
+        *qk_dst = bf16_bits_to_f32(qkr);
         __syncthreads();
         if (kNorm) {
             if (wave == 0) {
@@ -107,13 +121,13 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
         f32x4 a = part[0][0][cb] + part[1][0][cb] + part[2][0][cb] + part[3][0][cb];
         f32x4 bq = part[0][1][cb] + part[1][1][cb] + part[2][1][cb] + part[3][1][cb];
         const float decay = expf(gt);
-        const uint2 vraw = *reinterpret_cast<const uint2*>(v + (tk * HV + hv) * kDV + 4 * cb);
         f32x4 vv;
         vv[0] = bf16_bits_to_f32(vraw.x & 0xffffu);
         vv[1] = bf16_bits_to_f32(vraw.x >> 16);
         vv[2] = bf16_bits_to_f32(vraw.y & 0xffffu);
         vv[3] = bf16_bits_to_f32(vraw.y >> 16);
         const f32x4 delta = (vv - a * decay) * bt;
+        if (t + 1 < T) load_token(t + 1, qkr, vraw, gt, bt);
         if (rg == 0) {
             const f32x4 ov = (bq * decay + delta * kq) * scale;
             uint2 packed;
