@@ -334,11 +334,11 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update4_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) wf[e][j] = r[j];
         }
-        if (bias) {
-            const f32x4 r = *reinterpret_cast<const f32x4*>(static_cast<const float*>(bias) + d0);
+        // without a bias the same load reads the weights and is dropped: no
+        // branch, so every input load is issued before the first wait
+        const f32x4 r = *reinterpret_cast<const f32x4*>(static_cast<const float*>(bias ? bias : w) + d0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) bv[e] = r[e];
-        }
+        for (int e = 0; e < 4; ++e) bv[e] = bias ? r[e] : 0.f;
     } else {
         const u32x4* wp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w) + (size_t)d0 * 4);
 #pragma unroll
@@ -350,14 +350,19 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update4_kernel(
                 wf[2 * h + p / 2][2 * (p % 2) + 1] = hi16<WT>(r[p]);
             }
         }
-        if (bias) {
-            const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(bias) + d0);
-            bv[0] = lo16<WT>(r.x);
-            bv[1] = hi16<WT>(r.x);
-            bv[2] = lo16<WT>(r.y);
-            bv[3] = hi16<WT>(r.y);
-        }
+        const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(bias ? bias : w) + d0);
+        const bool hb = bias != nullptr;
+        bv[0] = hb ? lo16<WT>(r.x) : 0.f;
+        bv[1] = hb ? hi16<WT>(r.x) : 0.f;
+        bv[2] = hb ? lo16<WT>(r.y) : 0.f;
+        bv[3] = hb ? hi16<WT>(r.y) : 0.f;
     }
+    // token 0 of x before the state (the launcher returns before T = 0);
+    // each later token is requested while the previous one is computed
+    const uint16_t* xb = x + (size_t)b * xbs + d0;
+    uint16_t* yb = y + (size_t)b * ybs + d0;
+    __builtin_assume(T >= 1);
+    uint2 xr = *reinterpret_cast<const uint2*>(xb);
     // state rows: channel e's 4 tokens, oldest first, 8 bytes per channel
     uint16_t* st = state + (size_t)b * sbs + (size_t)d0 * 4;
     uint16_t win[4][4];   // [channel][slot]: the last 4 window tokens, oldest first
@@ -374,12 +379,10 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update4_kernel(
             win[e][3] = (uint16_t)(u >> 16);
         }
     }
-    const uint16_t* xb = x + (size_t)b * xbs + d0;
-    uint16_t* yb = y + (size_t)b * ybs + d0;
     for (int i = 0; i < T; ++i) {
-        const uint2 xr = *reinterpret_cast<const uint2*>(xb + (size_t)i * xts);
         const uint16_t xe[4] = {(uint16_t)xr.x, (uint16_t)(xr.x >> 16), (uint16_t)xr.y,
                                 (uint16_t)(xr.y >> 16)};
+        if (i + 1 < T) xr = *reinterpret_cast<const uint2*>(xb + (size_t)(i + 1) * xts);
         uint32_t out[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
