@@ -177,8 +177,11 @@ def bench_fused(ops, dev, steps, warmup):
 def bench_hf_lane(ops, dev, steps, warmup):
     """transformers' call into the fla adapter at T=1141, HV=32 (q/k already
     repeat_interleaved to 32 heads, bf16, use_qk_l2norm_in_kernel=True):
-    with the q/k normalisation in the prep kernel, and with it done by torch
-    first (the adapter's path for other dtypes or a custom scale)."""
+    with the q/k normalisation in the prep kernel (graph replay: device time,
+    as for the other secondaries; the call launches only this library's two
+    kernels), and with it done by torch first (the adapter's path for other
+    dtypes or a custom scale; timed eagerly, since torch's reductions are
+    kept out of captured graphs, so host launch time can show in it)."""
     import importlib
     import torch
     import gdn_cases as gc
@@ -198,7 +201,9 @@ def bench_hf_lane(ops, dev, steps, warmup):
     call = lambda i: ad.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0,  # noqa: E731
                                                output_final_state=True,
                                                use_qk_l2norm_in_kernel=True)
-    ms_k = time_calls(call, 1, max(10, steps // 4), warmup)
+    # 8 calls per captured graph, so the graph launch is amortised as in the
+    # other graph-timed workloads (same inputs each call: warm)
+    ms_k = time_graph(call, 8, max(4, steps // 16), warmup)
     call_t = lambda i: ad.chunk_gated_delta_rule(q, k, v, g, beta, scale=0.0883883,  # noqa: E731
                                                  initial_state=s0, output_final_state=True,
                                                  use_qk_l2norm_in_kernel=True)
@@ -478,7 +483,7 @@ def main():
                                                   "adapter_chain_us": round(fu["ms_c"] * 1e3, 2)},
             "hf_lane_chunk_gated_delta_rule_T1141_HV32": {
                 "us": round(hl["ms_k"] * 1e3, 2),
-                "us_torch_l2norm": round(hl["ms_t"] * 1e3, 2)},
+                "us_torch_l2norm_eager": round(hl["ms_t"] * 1e3, 2)},
             "causal_conv1d_update_B64x8192_k4": {"us": round(cv["ms_d"] * 1e3, 2),
                                                  "GB/s": round(cv["gbs_d"], 1),
                                                  "hbm_frac": round(cv["frac_d"], 4)},
