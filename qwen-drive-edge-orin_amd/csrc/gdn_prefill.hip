@@ -15,8 +15,8 @@
 // kernels/chunk_delta_cuda.cu:91-303 and :312-424 compute the same terms.)
 //
 // Two kernels:
-//   prep  one work-group per (chunk, v-head), three per CU: all chunk-local
-//         work.  K K^T and K Q^T run on bf16 MFMA straight from the bf16
+//   prep  one work-group per (chunk, v-head), up to four per CU: all
+//         chunk-local work.  K K^T and K Q^T run on bf16 MFMA straight from the bf16
 //         inputs; the inverse T is formed in fp32 in one LDS array (16x16
 //         diagonal blocks by forward substitution, off-diagonal blocks on
 //         fp32 MFMA, stored transposed in the free upper triangle).  Writes
