@@ -346,15 +346,22 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     // chunk's end read the last valid row (always in bounds) and are zeroed
     // afterwards, so no load sits behind a branch.  g and beta go first: the
     // gates need them before anything else arrives.
-    float gv = 0.f, bv = 0.f;
+    // Raw gate inputs are kept as loaded and turned into g and beta only
+    // after the K and Q loads are out: a use here would make wave 0 wait for
+    // them before it issues its share of K.
+    const bool raw_gate = kRaw != 0 && in.a != nullptr;
+    uint32_t ga = 0u, gb = 0u, gdt = 0u;
+    float gAl = 0.f;
     if (wave == 0) {
         const size_t gi = (size_t)(tok0 + min(lane, rows - 1)) * HV + hv;
-        if (kRaw == 0 || !in.a) {
-            gv = in.g[gi];
-            bv = in.beta[gi];
+        if (!raw_gate) {
+            ga = __float_as_uint(in.g[gi]);
+            gb = __float_as_uint(in.beta[gi]);
         } else {
-            gate_from_raw(raw16<kRaw>(in.a[gi]), raw16<kRaw>(in.b[gi]), in.A_log[hv],
-                          raw16<kRaw>(in.dt_bias[hv]), gv, bv);
+            ga = in.a[gi];
+            gb = in.b[gi];
+            gAl = in.A_log[hv];
+            gdt = in.dt_bias[hv];
         }
     }
     // K rows (16-byte pieces, row-major, bf16) go to LDS: thread t copies
@@ -381,6 +388,19 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
         }
     }
+    // opaque from here on: the compiler may not start the gate arithmetic
+    // (and so wait for its inputs) before the K and Q loads above
+    asm volatile("" : "+v"(ga), "+v"(gb), "+v"(gdt), "+v"(gAl)::"memory");
+    float gv = 0.f, bv = 0.f;
+    if (wave == 0) {
+        if (!raw_gate) {
+            gv = __uint_as_float(ga);
+            bv = __uint_as_float(gb);
+        } else {
+            gate_from_raw(raw16<kRaw>(ga), raw16<kRaw>(gb), gAl, raw16<kRaw>(gdt), gv, bv);
+        }
+    }
+
     if constexpr (kRaw != 0) {
         // raw inputs: K rows (16 lanes per row, 8 values each) and Q rows (4
         // lanes per row, 32 values each) L2-normalised and rounded to bf16
