@@ -240,14 +240,18 @@ def bench_conv(ops, dev, steps, warmup):
                 ms_d=ms_d, gbs_d=algo_d / ms_d / 1e6, frac_d=algo_d / ms_d / 1e6 / HBM_PEAK_GBS)
 
 
-# Algorithmic FLOPs per chunk-head of each prefill kernel (C = 64, dk = dv = 128,
-# 2 FLOP per MAC): prep forms K K^T, Q K^T, T (v beta), T (k beta e^c) and the
-# inversion (C^3/3 MACs); scan forms W S, (Q e^c) S, K~^T V_new and M V_new.
+# Algorithmic FLOPs per chunk-head of each prefill kernel under the fixed
+# convention (C = 64, dk = dv = 128, 2 FLOP per MAC; five C x C x 128
+# products, three 64 x 128 x 128 products and C^3/3 MACs of inversion, 182.95
+# kFLOP per token per v-head in total): prep forms K K^T, Q K^T and the
+# inversion; scan forms the rest -- the T (v beta) and T (k beta e^c) terms
+# (here T R with R = beta V - beta e^c K S), W S (here K S), (Q e^c) S,
+# K~^T V_new and M V_new.
 _CC = 2 * 64 * 64 * 128          # one C x C x 128 product
 _CD = 2 * 64 * 128 * 128         # one 64 x 128 x 128 product
 _INV = 2 * 64 ** 3 // 3
-KERNEL_FLOPS_PER_CHUNK_HEAD = {"gdn_prep_kernel": 4 * _CC + _INV,
-                               "gdn_scan_kernel": 3 * _CD + _CC}
+KERNEL_FLOPS_PER_CHUNK_HEAD = {"gdn_prep_kernel": 2 * _CC + _INV,
+                               "gdn_scan_kernel": 3 * _CD + 3 * _CC}
 
 
 class _Hip:
@@ -363,12 +367,29 @@ def profile_pass(ops, dev):
         ops.chunk_prefill(*sets[(7 * i) % len(sets)])
     torch.cuda.synchronize()
     del sets
+    # gated RMSNorm (1141 x 32 x 128) and the decode step (B64 HV32), each on
+    # input copies it has not touched before (cold)
+    x, z, w, eps = gc.rmsnorm_inputs()
+    nsets = rotation(lambda: (x, z, w), _bytes(x, z, w), dev)
+    for i in range(4):
+        ops.gated_rmsnorm(nsets[(5 * i) % len(nsets)][0], nsets[(5 * i) % len(nsets)][1],
+                          nsets[(5 * i) % len(nsets)][2], eps)
+    torch.cuda.synchronize()
+    del nsets
+    dq, dk, dv, dg, db, ds = gc.decode_inputs()
+    dsets = rotation(lambda: (dq, dk, dv, dg, db, ds), _bytes(dq, dk, dv, dg, db, ds), dev,
+                     max_sets=5)
+    for i in range(4):
+        ops.recurrent_step(*dsets[i % len(dsets)])
+    torch.cuda.synchronize()
+    del dsets
     src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(2):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    print("profile pass done: 4 prefill calls (T=1141, HV=32), 2 x torch.neg over 256 MiB", flush=True)
+    print("profile pass done: 4 prefill calls (T=1141, HV=32), 4 gated RMSNorm calls "
+          "(1141x32x128), 4 decode steps (B64 HV32), 2 x torch.neg over 256 MiB", flush=True)
 
 
 def cpu_baseline(budget_s=12.0):

@@ -40,47 +40,39 @@ extern "C" {
  * serves dump_debug = 0 and 1. */
 size_t deltanet_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int chunk_size);
 
+/* Workspace bytes for dump_debug = 0 only (no counterpart in the reference,
+ * whose size always includes its debug regions): a 256-byte header with the
+ * status word, then 12 KB per (chunk, v-head). */
+size_t deltanet_prefill_live_workspace_size(int B, int T, int HV, int DK, int DV,
+                                            int chunk_size);
+
 /* Chunked gated-delta-rule prefill.  Replaces deltanet_chunk_prefill,
  * kernels/chunk_delta_cuda.h:47-55 (same argument order and meaning; HIP
- * stream and error types).  initial_state may be NULL (zeros).
- * dump_debug != 0 additionally writes, past the live workspace, per chunk-head
- * fp32 T = (I - A)^-1 and A (each [B*NC*HV][64][64]) and the in-chunk cumsum
- * of g ([B*NC*HV][64]); chunk-head index = (b * NC + chunk) * HV + h. */
+ * stream and error types).  initial_state may be NULL (zeros); initial_state
+ * and final_state may be the same buffer.  workspace_bytes must be at least
+ * the live size (dump_debug = 0) or the full size (dump_debug != 0).
+ * dump_debug != 0 additionally writes, past the live workspace, per
+ * chunk-head (index (b * NC + chunk) * HV + h) fp32 T = (I - A)^-1, A, T right
+ * after the diagonal 16x16 blocks are inverted (A below them; the reference's
+ * post-leaf view), M = s (Q K^T o Gamma) (each [64][64]), the in-chunk cumsum
+ * of g ([64]) and the state at the chunk's start ([DK][DV]).
+ * The scan's waits are bounded: should one run out (another process holding
+ * the device, say) the call still completes, leaves o and final_state
+ * incomplete and sets the workspace's status word; deltanet_prefill_status
+ * reports it. */
 hipError_t deltanet_chunk_prefill(const void* q, const void* k, const void* v, const float* g,
                                   const float* beta, void* o, const float* initial_state,
                                   float* final_state, int B, int T, int HV, int HQK, int DK,
                                   int DV, int chunk_size, void* workspace, size_t workspace_bytes,
                                   hipStream_t stream, int dump_debug);
 
-/* Per-kernel timing of deltanet_chunk_prefill (no counterpart in the
- * reference; for benchmarks that attribute time to each kernel).
- * deltanet_prefill_kernel_count() kernels are launched; events[i] is recorded
- * on `stream` before kernel i and events[count] after the last, so
- * hipEventElapsedTime(events[i], events[i + 1]) is kernel i's duration.
- * n_events must equal count + 1; the other arguments are as in
- * deltanet_chunk_prefill (dump_debug = 0). */
-int deltanet_prefill_kernel_count(void);
-const char* deltanet_prefill_kernel_name(int i);
-hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k, const void* v,
-                                        const float* g, const float* beta, void* o,
-                                        const float* initial_state, float* final_state, int B,
-                                        int T, int HV, int HQK, int DK, int DV, int chunk_size,
-                                        void* workspace, size_t workspace_bytes,
-                                        hipStream_t stream, hipEvent_t* events, int n_events);
-
-/* One kernel of deltanet_chunk_prefill on its own (no counterpart in the
- * reference; for benchmarks that time back-to-back launches of a single
- * kernel).  kernel 0 (prep) fills the workspace from the inputs; kernel 1
- * (scan) reads a workspace that kernel 0 filled for the same arguments and
- * writes o and final_state.  Arguments as in deltanet_chunk_prefill
- * (dump_debug = 0); kernel outside [0, deltanet_prefill_kernel_count())
- * returns hipErrorInvalidValue. */
-hipError_t deltanet_chunk_prefill_kernel(const void* q, const void* k, const void* v,
-                                         const float* g, const float* beta, void* o,
-                                         const float* initial_state, float* final_state, int B,
-                                         int T, int HV, int HQK, int DK, int DV, int chunk_size,
-                                         void* workspace, size_t workspace_bytes,
-                                         hipStream_t stream, int kernel);
+/* Outcome of the last prefill call (any deltanet_chunk_prefill* entry) that
+ * used this workspace: synchronises `stream`, then returns hipSuccess, or
+ * hipErrorLaunchTimeOut when one of that call's bounded waits gave up (its o
+ * and final state are incomplete).  No counterpart in the reference, whose
+ * kernels do not wait on one another. */
+hipError_t deltanet_prefill_status(const void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream);
 
 /* Names of the reference's bf16-wmma o-pass twin (kernels/chunk_delta_cuda_tco.h:39,47);
  * same implementation and workspace as the two entries above. */
@@ -107,8 +99,8 @@ hipError_t deltanet_tcop_chunk_prefill(const void* q, const void* k, const void*
  *   state   : fp32 [B, HV, 128, 128], the initial state on entry and the
  *             final state on return (the adapter's h0_source)
  * q, k, v, a, b, dt_bias and o share io_dtype (GDN_DTYPE_FP16 as in the
- * plugin, or GDN_DTYPE_BF16).  The workspace is deltanet_prefill_workspace_size
- * bytes for the same B, T, HV. */
+ * plugin, or GDN_DTYPE_BF16).  The workspace is at least
+ * deltanet_prefill_live_workspace_size bytes for the same B, T, HV. */
 hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k, const void* v,
                                         const void* a, const void* b, const float* A_log,
                                         const void* dt_bias, void* o, float* state, int B, int T,
@@ -118,12 +110,17 @@ hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k, const void
 /* Variable-length prefill (no counterpart in the reference kernel: its torch
  * fallback drops cu_seqlens, transformers modeling_qwen3_5.py:259).
  * q, k, v, g, beta, o are packed [1, total_tokens, H, D]; cu_seqlens is a
- * device int32 [num_seqs + 1] with cu_seqlens[0] = 0, non-decreasing,
- * cu_seqlens[num_seqs] = total_tokens (the caller guarantees this; it is not
- * read on the host).  initial_state (or NULL) and final_state are
- * [num_seqs, HV, DK, DV].  Chunks never straddle sequences. */
+ * device int32 [num_seqs + 1], normally cu_seqlens[0] = 0, non-decreasing,
+ * cu_seqlens[num_seqs] = total_tokens; initial_state (or NULL) and
+ * final_state are [num_seqs, HV, DK, DV].  Chunks never straddle sequences.
+ * cu_seqlens is not read on the host; the kernels clamp every value into
+ * [0, total_tokens] and each sequence's end to no earlier than its start, and
+ * never form a chunk past the workspace's bound, so a malformed cu_seqlens
+ * gives wrong results but no access out of bounds. */
 size_t deltanet_prefill_varlen_workspace_size(int total_tokens, int num_seqs, int HV, int DK,
                                               int DV, int chunk_size);
+size_t deltanet_prefill_varlen_live_workspace_size(int total_tokens, int num_seqs, int HV,
+                                                   int DK, int DV, int chunk_size);
 hipError_t deltanet_chunk_prefill_varlen(const void* q, const void* k, const void* v,
                                          const float* g, const float* beta, void* o,
                                          const float* initial_state, float* final_state,
@@ -135,7 +132,7 @@ hipError_t deltanet_chunk_prefill_varlen(const void* q, const void* k, const voi
 
 /* deltanet_chunk_prefill (cu_seqlens NULL: B sequences of T tokens) or
  * deltanet_chunk_prefill_varlen (cu_seqlens set, B = 1, T = total tokens)
- * with raw bf16 q and k rows, L2-normalised inside the prep kernel as
+ * with raw bf16 q and k rows, L2-normalised inside the kernels as
  * x rsqrt(sum x^2 + 1e-6) in fp32 and rounded to bf16 -- transformers'
  * use_qk_l2norm_in_kernel=True (models/qwen3_5/modeling_qwen3_5.py:242-245,
  * 270-271).  No counterpart in the reference kernel, whose callers normalise

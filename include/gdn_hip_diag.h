@@ -1,0 +1,72 @@
+/*
+ * Diagnostic entry points of libgdn_hip.so: per-kernel timing, a bounded-wait
+ * test hook and the host mirror of the varlen chunk bookkeeping.  None is part
+ * of the drop-in boundary (include/gdn_hip.h) and none has a counterpart in
+ * the reference; benchmarks and tests use them.  Conventions as in gdn_hip.h.
+ */
+#ifndef GDN_HIP_DIAG_H_
+#define GDN_HIP_DIAG_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-kernel timing of deltanet_chunk_prefill (for benchmarks that attribute
+ * time to each kernel).  deltanet_prefill_kernel_count() kernels are launched;
+ * events[i] is recorded on `stream` before kernel i and events[count] after
+ * the last, so hipEventElapsedTime(events[i], events[i + 1]) is kernel i's
+ * duration.  n_events must equal count + 1; the other arguments are as in
+ * deltanet_chunk_prefill (dump_debug = 0). */
+int deltanet_prefill_kernel_count(void);
+const char* deltanet_prefill_kernel_name(int i);
+hipError_t deltanet_chunk_prefill_timed(const void* q, const void* k, const void* v,
+                                        const float* g, const float* beta, void* o,
+                                        const float* initial_state, float* final_state, int B,
+                                        int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                        void* workspace, size_t workspace_bytes,
+                                        hipStream_t stream, hipEvent_t* events, int n_events);
+
+/* One kernel of deltanet_chunk_prefill on its own (for benchmarks that time
+ * back-to-back launches of a single kernel).  kernel 0 (prep) fills the
+ * workspace from the inputs; kernel 1 (scan) reads a workspace that kernel 0
+ * filled for the same arguments and writes o and final_state.  Arguments as
+ * in deltanet_chunk_prefill (dump_debug = 0); kernel outside
+ * [0, deltanet_prefill_kernel_count()) returns hipErrorInvalidValue. */
+hipError_t deltanet_chunk_prefill_kernel(const void* q, const void* k, const void* v,
+                                         const float* g, const float* beta, void* o,
+                                         const float* initial_state, float* final_state, int B,
+                                         int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                         void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream, int kernel);
+
+/* deltanet_chunk_prefill (DK = DV = 128, chunk 64, dump_debug = 0) with the
+ * scan's bounded waits limited to spin_limit polls each (the library's own
+ * limit is 2^20).  With a small limit the waits give up, every kernel still
+ * returns normally, and deltanet_prefill_status then reports
+ * hipErrorLaunchTimeOut: the test of that error path. */
+hipError_t deltanet_chunk_prefill_spin(const void* q, const void* k, const void* v,
+                                       const float* g, const float* beta, void* o,
+                                       const float* initial_state, float* final_state, int B,
+                                       int T, int HV, int HQK, void* workspace,
+                                       size_t workspace_bytes, hipStream_t stream,
+                                       unsigned spin_limit);
+
+/* Host mirror of the kernels' sequence bookkeeping for a packed batch
+ * (host memory, no GPU involved): for each sequence s its first chunk id,
+ * the chunks the scan processes (never past the workspace's chunk bound),
+ * its first token and its token count after clamping cu_seqlens into
+ * [0, total_tokens].  Returns the workspace's chunk bound per head, or -1 for
+ * invalid arguments.  Runs the same code as the kernels (gdn_seq.h). */
+int deltanet_varlen_chunk_map(const int32_t* cu_seqlens, int num_seqs, int total_tokens,
+                              int32_t* seq_first_chunk, int32_t* seq_chunk_count,
+                              int32_t* seq_first_token, int32_t* seq_token_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_HIP_DIAG_H_ */

@@ -13,6 +13,8 @@ transformers 5.14.1 ``models/qwen3_5/modeling_qwen3_5.py``:
 
 * ``l2norm``                 -> modeling_qwen3_5.py:242-245
 * ``chunk_gated_delta_rule`` -> modeling_qwen3_5.py:249-327 (== parity_test.py:35-96)
+* ``chunk_debug_views``      -> the per-chunk A, T, M, cumsum(g) and entry states of the
+                                same computation, as kernels/torch_binding.cpp:58-86 exposes them
 * ``recurrent_gated_delta_rule`` -> modeling_qwen3_5.py:331-380
 * ``gated_rmsnorm``          -> modeling_qwen3_5.py:168-184 (Qwen3_5RMSNormGated)
 * ``causal_conv1d``          -> modeling_qwen3_5.py:219-240 (causal_conv1d_fn)
@@ -51,6 +53,7 @@ __all__ = [
     "expand_kv_heads",
     "chunk_gated_delta_rule",
     "chunk_gated_delta_rule_varlen",
+    "chunk_debug_views",
     "recurrent_gated_delta_rule",
     "recurrence_fp64",
     "gated_rmsnorm",
@@ -104,7 +107,7 @@ def unit_lower_inverse(A: torch.Tensor) -> torch.Tensor:
     return X + torch.eye(C, dtype=A.dtype)
 
 
-def _chunk_core(q, k, v, g, beta, chunk_size, s0, dtype):
+def _chunk_core(q, k, v, g, beta, chunk_size, s0, dtype, views=None):
     """Chunked gated delta rule on [B, H, T, D] fp tensors (heads already
     expanded).  Restates modeling_qwen3_5.py:262-327 term by term:
 
@@ -150,10 +153,15 @@ def _chunk_core(q, k, v, g, beta, chunk_size, s0, dtype):
 
     S = torch.zeros(B, H, DK, DV, dtype=dtype) if s0 is None else s0.to(dtype).clone()
     out = torch.empty(B, H, n, chunk_size, DV, dtype=dtype)
+    if views is not None:
+        views.update(A=A, T=Tm, c=c, M=[], S=[])
     for i in range(n):
         qi, ki = qc[:, :, i], kc[:, :, i]
         ci = c[:, :, i]
         M = (qi @ ki.transpose(-1, -2)) * gamma[:, :, i]
+        if views is not None:
+            views["M"].append(M)
+            views["S"].append(S.clone())
         v_new = U[:, :, i] - W[:, :, i] @ S
         out[:, :, i] = (qi * ci.exp().unsqueeze(-1)) @ S + M @ v_new
         last = ci[..., -1:]
@@ -182,6 +190,28 @@ def chunk_gated_delta_rule(q, k, v, g, beta, initial_state=None, chunk_size=64,
     o, S = _chunk_core(tr(q), tr(k), tr(v), tr(g), tr(beta), chunk_size,
                        initial_state, dtype)
     return o.transpose(1, 2).contiguous(), S
+
+
+def chunk_debug_views(q, k, v, g, beta, initial_state=None, chunk_size=64,
+                      dtype=torch.float64):
+    """Per-chunk quantities of ``chunk_gated_delta_rule`` for one sequence
+    (B = 1), as the reference's debug workspace exposes them
+    (kernels/torch_binding.cpp:58-86): A, T = (I - A)^-1, M = s (Q K^T o
+    Gamma), the in-chunk cumsum of g, and the state at each chunk's start.
+    Returns a dict of tensors [NC, HV, ...] (A, T, M: [..., C, C]; c: [..., C];
+    S: [..., DK, DV]), padded rows included as the kernels pad them."""
+    assert q.shape[0] == 1, "one sequence"
+    HV = v.shape[2]
+    qx = expand_kv_heads(q.to(dtype), HV)
+    kx = expand_kv_heads(k.to(dtype), HV)
+    tr = lambda x: x.transpose(1, 2).contiguous().to(dtype)  # noqa: E731
+    views = {}
+    _chunk_core(tr(qx), tr(kx), tr(v), tr(g), tr(beta), chunk_size, initial_state, dtype,
+                views=views)
+    first = lambda x: x[0].transpose(0, 1).contiguous()  # noqa: E731  [H, n, ...] -> [n, H, ...]
+    return dict(A=first(views["A"]), T=first(views["T"]), c=first(views["c"]),
+                M=torch.stack([m[0] for m in views["M"]], 0),
+                S=torch.stack([x[0] for x in views["S"]], 0))
 
 
 def chunk_gated_delta_rule_varlen(q, k, v, g, beta, cu_seqlens, initial_state=None,

@@ -1,0 +1,54 @@
+// Sequence and chunk bookkeeping of the chunked prefill, shared by the
+// kernels (device) and deltanet_varlen_chunk_map (host, for tests).
+//
+// Packed variable-length batches give cu_seqlens [N + 1].  Every value is
+// clamped into [0, total_tokens] and a sequence's end is clamped to be no
+// earlier than its start, so any cu_seqlens -- including a non-monotone or
+// out-of-range one -- gives token ranges inside [0, total_tokens).  Chunk ids
+// at or past the workspace's chunk bound are never formed: the prep skips
+// them and the scan truncates a sequence that would reach them.  Malformed
+// input thus gives wrong results, never an access out of bounds.  Fixed-length
+// batches (cu == nullptr) are N sequences of T tokens, cu[i] = i * T.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define GDN_HD __host__ __device__
+#else
+#define GDN_HD
+#endif
+
+namespace gdn {
+
+constexpr int kChunkRows = 64;
+
+GDN_HD inline int clamp_tok(int32_t x, int total) { return x < 0 ? 0 : (x > total ? total : (int)x); }
+
+// First token of sequence s.
+GDN_HD inline int seq_lo(const int32_t* cu, int T, int total, int s) {
+    return cu ? clamp_tok(cu[s], total) : s * T;
+}
+
+// Token count of sequence s (>= 0).
+GDN_HD inline int seq_count(const int32_t* cu, int T, int total, int s) {
+    if (!cu) return T;
+    const int lo = clamp_tok(cu[s], total), hi = clamp_tok(cu[s + 1], total);
+    return hi > lo ? hi - lo : 0;
+}
+
+GDN_HD inline int seq_chunks(const int32_t* cu, int T, int total, int s) {
+    const int n = seq_count(cu, T, total, s);
+    return n / kChunkRows + (n % kChunkRows != 0);   // no n + 63 overflow near INT_MAX
+}
+
+// Chunks a sequence may use when its first chunk id is chunk0 and the
+// workspace holds nch_bound chunks per head.
+GDN_HD inline int seq_chunks_bounded(const int32_t* cu, int T, int total, int s, int chunk0,
+                                     int nch_bound) {
+    const int n = seq_chunks(cu, T, total, s);
+    const int room = nch_bound - chunk0;
+    return room <= 0 ? 0 : (n < room ? n : room);
+}
+
+}  // namespace gdn

@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "gdn_hip.h"
+#include "gdn_hip_diag.h"
 
 namespace {
 
@@ -40,7 +41,8 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
                                            const at::Tensor& beta,
                                            const std::optional<at::Tensor>& s0,
                                            const std::optional<at::Tensor>& cu_seqlens,
-                                           bool debug, bool qk_l2norm = false) {
+                                           bool debug, bool qk_l2norm = false,
+                                           bool checked = false, int64_t spin = -1) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda(),
                 "all inputs must be CUDA tensors");
     TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
@@ -92,15 +94,27 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
         s0p = s0c.data_ptr<float>();
     }
 
+    // the debug tail only when the views are asked for
     const size_t ws_bytes =
         cu_seqlens.has_value()
-            ? deltanet_prefill_varlen_workspace_size((int)T, (int)N, (int)HV, (int)DK, (int)DV, kChunk)
-            : deltanet_prefill_workspace_size((int)B, (int)T, (int)HV, (int)DK, (int)DV, kChunk);
+            ? (debug ? deltanet_prefill_varlen_workspace_size
+                     : deltanet_prefill_varlen_live_workspace_size)((int)T, (int)N, (int)HV,
+                                                                    (int)DK, (int)DV, kChunk)
+            : (debug ? deltanet_prefill_workspace_size : deltanet_prefill_live_workspace_size)(
+                  (int)B, (int)T, (int)HV, (int)DK, (int)DV, kChunk);
     TORCH_CHECK(ws_bytes > 0, "unsupported prefill configuration");
     auto ws = at::empty({(int64_t)ws_bytes}, vc.options().dtype(at::kByte));
 
     hipError_t err;
-    if (qk_l2norm) {
+    if (spin >= 0) {
+        TORCH_CHECK(!qk_l2norm && !cu_seqlens.has_value() && !debug,
+                    "the spin-limit test entry takes the plain fixed-length form");
+        err = deltanet_chunk_prefill_spin(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                          gc.data_ptr<float>(), bc.data_ptr<float>(), o.data_ptr(),
+                                          s0p, sf.data_ptr<float>(), (int)B, (int)T, (int)HV,
+                                          (int)HQK, ws.data_ptr(), ws_bytes, current_stream(),
+                                          (unsigned)spin);
+    } else if (qk_l2norm) {
         err = deltanet_chunk_prefill_l2norm(
             qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr<float>(), bc.data_ptr<float>(),
             o.data_ptr(), s0p, sf.data_ptr<float>(),
@@ -120,24 +134,38 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
                                      current_stream(), debug ? 1 : 0);
     }
     check_hip(err, "deltanet_chunk_prefill");
+    if (checked || spin >= 0) {
+        const hipError_t st = deltanet_prefill_status(ws.data_ptr(), ws_bytes, current_stream());
+        if (spin >= 0) {
+            // test entry: the status is returned, not raised
+            auto flag = at::full({1}, st == hipSuccess ? 0 : 1, vc.options().dtype(at::kInt));
+            return {o, sf, flag};
+        }
+        check_hip(st, "deltanet_chunk_prefill (status word)");
+    }
 
     std::vector<at::Tensor> out{o, sf};
     if (debug) {
-        // debug tail: [T | A | cumsum(g)] per chunk-head, the last three
-        // regions of the workspace (each 256-byte aligned, see gdn_prefill.hip)
+        // debug tail, the last six regions of the workspace, each 256-byte
+        // aligned (gdn_prefill.hip WsLayout): per chunk-head fp32 T, A,
+        // T after the diagonal blocks, M ([64][64] each), cumsum(g) [64] and
+        // the state at the chunk's start [128][128]
         const int64_t nc = cu_seqlens.has_value() ? (T + (int64_t)(kChunk - 1) * N) / kChunk
                                                   : B * ((T + kChunk - 1) / kChunk);
         const int64_t nch = nc * HV;
         auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
-        const int64_t tail = al(nch * kChunk * kChunk * 4) * 2 + al(nch * kChunk * 4);
-        const int64_t off = (int64_t)ws_bytes - tail;
+        const int64_t sq = al(nch * kChunk * kChunk * 4), sc = al(nch * kChunk * 4),
+                      ss = al(nch * DK * DV * 4);
+        const int64_t off = (int64_t)ws_bytes - (4 * sq + sc + ss);
         auto wsf = [&](int64_t byte_off, int64_t count) {
             return ws.narrow(0, byte_off, count * 4).view(at::kFloat);
         };
-        out.push_back(wsf(off, nch * kChunk * kChunk).view({nc, HV, kChunk, kChunk}));
-        out.push_back(wsf(off + al(nch * kChunk * kChunk * 4), nch * kChunk * kChunk)
-                          .view({nc, HV, kChunk, kChunk}));
-        out.push_back(wsf(off + 2 * al(nch * kChunk * kChunk * 4), nch * kChunk).view({nc, HV, kChunk}));
+        out.push_back(wsf(off, nch * kChunk * kChunk).view({nc, HV, kChunk, kChunk}));            // T
+        out.push_back(wsf(off + sq, nch * kChunk * kChunk).view({nc, HV, kChunk, kChunk}));       // A
+        out.push_back(wsf(off + 4 * sq, nch * kChunk).view({nc, HV, kChunk}));                   // cumsum g
+        out.push_back(wsf(off + 2 * sq, nch * kChunk * kChunk).view({nc, HV, kChunk, kChunk}));   // T post-leaf
+        out.push_back(wsf(off + 3 * sq, nch * kChunk * kChunk).view({nc, HV, kChunk, kChunk}));   // M
+        out.push_back(wsf(off + 4 * sq + sc, nch * DK * DV).view({nc, HV, DK, DV}));              // S_c
     }
     return out;
 }
@@ -146,8 +174,21 @@ std::vector<at::Tensor> chunk_prefill_impl(const at::Tensor& q, const at::Tensor
 
 std::vector<at::Tensor> chunk_prefill(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
                                       at::Tensor beta, std::optional<at::Tensor> s0,
-                                      std::optional<at::Tensor> cu_seqlens, bool qk_l2norm) {
-    return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/false, qk_l2norm);
+                                      std::optional<at::Tensor> cu_seqlens, bool qk_l2norm,
+                                      bool checked) {
+    return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/false, qk_l2norm,
+                              checked);
+}
+
+// Test entry: the plain prefill with the scan's bounded waits limited to
+// `spin` polls; returns [o, final_state, status] with status 1 when a wait
+// gave up (o and final_state are then incomplete).
+std::vector<at::Tensor> chunk_prefill_spin_limit(at::Tensor q, at::Tensor k, at::Tensor v,
+                                                 at::Tensor g, at::Tensor beta,
+                                                 std::optional<at::Tensor> s0, int64_t spin) {
+    TORCH_CHECK(spin >= 0, "spin must be >= 0");
+    return chunk_prefill_impl(q, k, v, g, beta, s0, std::nullopt, /*debug=*/false, false, false,
+                              spin);
 }
 
 std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tensor v,
@@ -259,7 +300,7 @@ at::Tensor chunk_prefill_fused(at::Tensor q, at::Tensor k, at::Tensor v, at::Ten
     auto Ac = A_log.contiguous(), dc = dt_bias.contiguous();
     auto o = at::empty_like(vc);
     const size_t ws_bytes =
-        deltanet_prefill_workspace_size((int)B, (int)T, (int)HV, 128, 128, kChunk);
+        deltanet_prefill_live_workspace_size((int)B, (int)T, (int)HV, 128, 128, kChunk);
     TORCH_CHECK(ws_bytes > 0 || T == 0, "unsupported prefill configuration");
     auto ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 256)}, vc.options().dtype(at::kByte));
     check_hip(deltanet_chunk_prefill_fused(
@@ -360,11 +401,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "chunked gated delta rule prefill (gfx950 HIP); returns [o, final_state]; qk_l2norm: "
           "q and k rows are raw and L2-normalised in the kernel",
           "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
-          "cu_seqlens"_a = std::nullopt, "qk_l2norm"_a = false);
+          "cu_seqlens"_a = std::nullopt, "qk_l2norm"_a = false, "checked"_a = false);
     m.def("chunk_prefill_debug", &chunk_prefill_debug,
-          "same, also returns per-chunk-head T=(I-A)^-1, A and cumsum(g) views", "q"_a, "k"_a,
-          "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
+          "same, also returns per-chunk-head views: T=(I-A)^-1, A, cumsum(g), T after the "
+          "diagonal-block inversion, M, and the state at each chunk's start",
+          "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
           "cu_seqlens"_a = std::nullopt);
+    m.def("_chunk_prefill_spin_limit", &chunk_prefill_spin_limit,
+          "test entry: prefill with the scan's bounded waits limited to `spin` polls; returns "
+          "[o, final_state, status]",
+          "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "s0"_a, "spin"_a);
     m.def("recurrent_step", &recurrent_step,
           "recurrent gated delta rule (decode), state updated in place; returns o", "q"_a, "k"_a,
           "v"_a, "g"_a, "beta"_a, "state"_a, pybind11::kw_only(), "qk_l2norm"_a = false);

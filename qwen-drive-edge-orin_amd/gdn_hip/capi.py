@@ -1,4 +1,4 @@
-"""ctypes view of libgdn_hip.so's C ABI (include/gdn_hip.h).
+"""ctypes view of libgdn_hip.so's C ABI (include/gdn_hip.h, include/gdn_hip_diag.h).
 
 This is the binding a Python caller of the reference's C entry points would
 write; the tests use it to call the boundary directly with raw device
@@ -12,7 +12,8 @@ from pathlib import Path
 
 from . import LIB_PATH
 
-HEADER = Path(__file__).resolve().parents[2] / "include" / "gdn_hip.h"
+INCLUDE = Path(__file__).resolve().parents[2] / "include"
+HEADERS = sorted(INCLUDE.glob("*.h"))
 
 hipError_t = ct.c_int
 hipStream_t = ct.c_void_p
@@ -21,6 +22,7 @@ c_int, c_size_t, c_int64, c_float = ct.c_int, ct.c_size_t, ct.c_int64, ct.c_floa
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
+HIP_ERROR_LAUNCH_TIMEOUT = 702
 DTYPE_BF16, DTYPE_FP16, DTYPE_FP32 = 0, 1, 2
 
 _PROTOS = {
@@ -30,7 +32,13 @@ _PROTOS = {
                                [vp, c_size_t, hipStream_t, c_int]),
     "deltanet_tcop_chunk_prefill": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
                                     [vp, c_size_t, hipStream_t, c_int]),
+    "deltanet_prefill_live_workspace_size": (c_size_t, [c_int] * 6),
     "deltanet_prefill_varlen_workspace_size": (c_size_t, [c_int] * 6),
+    "deltanet_prefill_varlen_live_workspace_size": (c_size_t, [c_int] * 6),
+    "deltanet_prefill_status": (hipError_t, [vp, c_size_t, hipStream_t]),
+    "deltanet_chunk_prefill_spin": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 4 +
+                                    [vp, c_size_t, hipStream_t, ct.c_uint]),
+    "deltanet_varlen_chunk_map": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
     "deltanet_chunk_prefill_varlen": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, i32p] +
                                       [c_int] * 7 + [vp, c_size_t, hipStream_t, c_int]),
     "deltanet_recurrent_step": (hipError_t, [vp, vp, vp, fp, fp, vp, fp] + [c_int] * 6 +
@@ -57,11 +65,13 @@ _PROTOS = {
 
 
 def declared_symbols() -> list[str]:
-    """Function names declared in include/gdn_hip.h."""
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^\s*(?:size_t|hipError_t|int|const char\s*\*)\s*(\w+)\s*\(", text,
-                      flags=re.M)
+    """Function names declared in include/*.h."""
+    names = []
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:size_t|hipError_t|int|const char\s*\*)\s*(\w+)\s*\(",
+                            text, flags=re.M)
+    return names
 
 
 _lib = None

@@ -127,6 +127,37 @@ def test_unit_lower_inverse_matches_solve_triangular():
     assert _err(X, ref) < 1e-10
 
 
+def test_chunk_debug_views_pinned():
+    """chunk_debug_views: T against solve_triangular(I - A); the chunk-entry
+    states against the independent fp64 token recurrence run over each
+    prefix; M through the first chunk's closed form o = M T diag(beta) V
+    (zero initial state), with o from that same recurrence; c as the per-chunk
+    cumulative sum of g."""
+    q, k, v, g, beta, s0 = [t.double() for t in gc.make_gdn_inputs(21, B=1, T=150, HK=1, HV=2,
+                                                                  D=32)]
+    views = orc.chunk_debug_views(q, k, v, g, beta, s0, dtype=torch.float64)
+    A, Tm, M, c, S = views["A"], views["T"], views["M"], views["c"], views["S"]
+    nc = 3
+    assert A.shape == (nc, 2, 64, 64) and S.shape == (nc, 2, 32, 32) and c.shape == (nc, 2, 64)
+    eye = torch.eye(64, dtype=torch.float64)
+    inv = torch.linalg.solve_triangular(eye - A, eye, upper=False, unitriangular=True)
+    assert torch.allclose(Tm, inv, atol=1e-12)
+    for n in range(nc):
+        if n == 0:
+            ref = s0.double()[0]
+        else:
+            _, sr = orc.recurrence_fp64(q[:, :64 * n], k[:, :64 * n], v[:, :64 * n],
+                                        g[:, :64 * n], beta[:, :64 * n], s0)
+            ref = torch.from_numpy(sr[0])
+        assert torch.allclose(S[n], ref, atol=1e-10), n
+    gp = F.pad(g.double(), (0, 0, 0, 42))[0].reshape(nc, 64, 2).permute(0, 2, 1)
+    assert torch.allclose(c, gp.cumsum(-1), atol=1e-12)
+    o_rec, _ = orc.recurrence_fp64(q[:, :64], k[:, :64], v[:, :64], g[:, :64], beta[:, :64])
+    vb = v[0, :64].double().permute(1, 0, 2) * beta[0, :64].double().t().unsqueeze(-1)
+    o_m = M[0] @ (Tm[0] @ vb)                      # [H, 64, DV]
+    assert torch.allclose(o_m, torch.from_numpy(o_rec[0]).permute(1, 0, 2), atol=1e-10)
+
+
 def test_varlen_is_independent_per_sequence():
     lens = [0, 1, 63, 70, 5]
     cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
