@@ -8,38 +8,44 @@
 //   c   = cumsum(g)            Gamma_rj = exp(c_r - c_j)  (r >= j)
 //   A   = -diag(beta) (K K^T o Gamma)  strictly lower,   T = (I - A)^-1
 //   M   = s (Q K^T o Gamma)    lower incl. diagonal
-//   V_n = T diag(beta) V - T diag(beta e^c) K S           (= U - W S)
+//   U   = T diag(beta) V,      W = T diag(beta e^c) K
+//   V_n = U - W S
 //   O   = diag(s e^c) Q S + M V_n
 //   S  <- e^{c_63} S + K^T diag(e^{c_63 - c}) V_n
 //
 // (transformers modeling_qwen3_5.py:249-327, the reference's parity oracle;
 // kernels/chunk_delta_cuda.cu:91-303, :312-424 and :532-674 compute the same
-// terms with U, W and the decayed K kept in a workspace.)
-//
-// Here V_n is formed T-factored: R = beta o V - (beta e^c) o (K S), then
-// V_n = R + (T - I) R.  The scan therefore needs only T - I and M per
-// chunk-head from the prep (12 KB, fp16 fragments); K, Q and V come straight
-// from the inputs.  The state update K^T (d o V_n) takes d o V_n as an fp16
-// hi/lo pair, whose lo part goes to a second accumulator off the serial path.
+// terms.)
 //
 // Two kernels:
-//   prep  one work-group per (chunk, v-head): gates, K K^T and Q K^T on bf16
+//   prep  one work-group per (chunk, v-head): gates, K K^T and Q K^T on fp16
 //         MFMA, the inverse T in fp32 (16x16 diagonal blocks by forward
-//         substitution, off-diagonal blocks on fp32 MFMA), then T - I and M as
-//         fp16 MFMA fragments.
-//   scan  four work-groups per (sequence, v-head), each owning 32 value
-//         columns of the state as two 16-column slices.  Per chunk a chain
-//         wave per slice forms P = K S, V_n and S', with S in registers for the
-//         whole sequence; one output wave forms O for both slices; three
-//         loader waves stream K and Q (converted to fp16), V, T - I, M and the
-//         gates into LDS rings.  Waves meet through LDS counters with bounded
-//         waits; a wait that runs out aborts the work-group and sets the
-//         workspace's status word (deltanet_prefill_status).
+//         substitution, off-diagonal blocks on fp32 MFMA), then -W (fp16,
+//         from W^T = K^T (T diag(beta e^c))^T on fp16 MFMA), T - I as an
+//         fp16 hi / lo pair, M, a gates record, and Q as fp16 fragments.
+//   scan  one work-group per (16 value columns, v-head, sequence), four
+//         waves on four SIMDs: a chain wave keeps the 128 x 16 state slice
+//         in registers and per chunk forms V_n = U - W S (fp16 MFMA, U the
+//         accumulator's fp32 initial value) and S <- e^{c63} S + K^T (d V_n)
+//         (bf16 MFMA on the input K, d V_n as a bf16 hi / lo pair, the lo
+//         part into a second accumulator off the serial path); a producer
+//         wave forms U = beta V + (T - I)(beta V) from hi / lo fp16 products;
+//         an output wave forms O; a loader wave moves K, -W, V and the gates
+//         into a three-stage LDS ring with direct-to-LDS loads.  Waves meet
+//         through LDS counters with bounded waits; a wait that runs out aborts
+//         the work-group and sets the workspace's status word
+//         (deltanet_prefill_status).
+//
+// Rounding budget (checked against an fp64 emulation of each operand class):
+// W and S rounded to fp16 for V_n change the final state by < 1e-4 relative;
+// U, and d V_n in the state update, are kept to ~16 bits or more, since a
+// single fp16 rounding of either gives 1.4 - 2.7e-3.
 //
 // The fused entry (deltanet_chunk_prefill_fused) and the l2norm entry run the
-// same kernels on raw inputs: both kernels L2-normalise q and k rows as they
-// load them, convert fp16 inputs, form g and beta from the gate inputs, and
-// the scan stores o in the I/O dtype and the final state over the initial one.
+// same kernels on raw inputs: the prep L2-normalises q and k rows as it loads
+// them, converts fp16 inputs, forms g and beta from the gate inputs and
+// writes the normalised k rows for the scan; the scan stores o in the I/O
+// dtype and the final state over the initial one.
 #include "gdn_common.h"
 #include "gdn_hip.h"
 #include "gdn_hip_diag.h"
@@ -53,25 +59,43 @@ namespace gdn {
 namespace {
 
 constexpr int kPrepThreads = 256;
-constexpr int kScanThreads = 512;
-constexpr int kPairCols = 32;                      // value columns per scan work-group
-constexpr int kPairsPerHead = kDV / kPairCols;     // 4
+constexpr int kScanThreads = 256;
+constexpr int kSliceCols = 16;                     // value columns per scan work-group
+constexpr int kSlicesPerHead = kDV / kSliceCols;   // 8
 constexpr int kTri = 6;                            // nonzero (row tile, k-block) fragments of a lower-triangular 64x64
-constexpr int kGateDecay = 64;
 constexpr unsigned kDefaultSpin = 1u << 20;        // bounded waits: ~0.1 s of polling, then give up
 
 // First fragment index of row tile mt among the kTri lower-triangular ones:
 // (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
 __host__ __device__ constexpr int tri_base(int mt) { return mt < 3 ? mt : 4; }
 
-// Per chunk-head workspace record: (T - I) and M, kTri A-fragments each (fp16,
-// 16 bytes per lane).  A 256-byte header in front holds the status word.
-constexpr size_t kTriBytes = (size_t)kTri * 64 * 16;   // 6 KB
+// Per chunk-head workspace records (fp16 fragments, 16 bytes per lane):
+//   TI, TIlo  (T - I) as hi / lo pair       kTri fragments each     6 KB each
+//   M                                        kTri fragments          6 KB
+//   W         -W, row tile mt, k-block kb   16 fragments            16 KB
+//   gates     beta, d = e^{c63 - c}, s e^c, c63                      1 KB
+//   Q         Q rows as fp16 fragments, per (chunk, k-head)          16 KB
+//   Kn        normalised k rows (raw-input entries), [token][HK][128] bf16
+// A 256-byte header in front holds the status word.
+constexpr size_t kFrag = 64 * 16;                      // one fragment: 1 KB
+constexpr size_t kTriBytes = (size_t)kTri * kFrag;     // 6 KB
+constexpr size_t kWBytes = 16 * kFrag;                 // 16 KB
+constexpr size_t kGateBytes = 1024;
+constexpr size_t kQBytes = 16 * kFrag;                 // 16 KB
+constexpr size_t kKnBytes = (size_t)kChunk * kDK * 2;  // 16 KB of k rows per chunk-head bound
 constexpr size_t kHeaderBytes = 256;
 
+// gates record: float offsets
+constexpr int kGBeta = 0, kGDec = 64, kGSec = 128, kGC63 = 192;
+
 struct Workspace {
-    half8* TI;          // (T - I) fragments [chunk-head][kTri][64]
+    half8* TI;          // (T - I) hi fragments [chunk-head][kTri][64]
+    half8* TIlo;        // (T - I) lo fragments, same layout
     half8* M;           // M fragments, same layout
+    half8* W;           // -W fragments [chunk-head][mt * 4 + kb][64]
+    float* gates;       // [chunk-head][256]
+    half8* Q;           // Q fragments [chunk * HK + hk][mt * 4 + kb][64]
+    uint16_t* Kn;       // normalised k rows (raw-input entries) [token][HK][128]
     unsigned* status;   // bit 0: a bounded wait gave up
     float* dbgT;        // optional [chunk-head][64][64]: T = (I - A)^-1
     float* dbgA;        // optional: A
@@ -86,11 +110,16 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 // Byte layout of the workspace for `nch` chunk-heads.  The debug regions stay
 // last: the torch binding finds them from the end.
 struct WsLayout {
-    size_t ti, m, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
+    size_t ti, tilo, m, w, gates, q, kn, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
     __host__ explicit WsLayout(size_t nch) {
         size_t off = kHeaderBytes;
         ti = off;    off += align256(nch * kTriBytes);
+        tilo = off;  off += align256(nch * kTriBytes);
         m = off;     off += align256(nch * kTriBytes);
+        w = off;     off += align256(nch * kWBytes);
+        gates = off; off += align256(nch * kGateBytes);
+        q = off;     off += align256(nch * kQBytes);
+        kn = off;    off += align256(nch * kKnBytes);
         live = off;
         dbgT = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgA = off;  off += align256(nch * kChunk * kChunk * 4);
@@ -142,46 +171,35 @@ __device__ inline void gate_from_raw(float a, float b, float A_log, float dt_bia
     beta = 1.f / (1.f + expf(-b));
 }
 
-// g and beta of one token of v-head hv (index gi = token * HV + hv).
+// Eight 16-bit elements of a 128-wide row (one 16-byte piece) as fp32, the
+// row spread over `kLanes` lanes of consecutive lane ids xor-masks (16 lanes
+// for one piece per lane, or lanes 16 apart for four pieces per lane).  For
+// kRaw != 0 the row is L2-normalised, x rsqrt(sum x^2 + 1e-6) in fp32, and
+// rounded to bf16 (the reference adapter's normalisation,
+// gdnChunkPrefillSm87.cu:52-84; transformers l2norm, modeling_qwen3_5.py:
+// 242-245).
 template <int kRaw>
-__device__ inline void load_gate(const PrepIn& in, size_t gi, int hv, float& g, float& beta) {
-    if (kRaw != 0 && in.a != nullptr) {
-        gate_from_raw(raw16<kRaw>(in.a[gi]), raw16<kRaw>(in.b[gi]), in.A_log[hv],
-                      raw16<kRaw>(in.dt_bias[hv]), g, beta);
-    } else {
-        g = in.g[gi];
-        beta = in.beta[gi];
-    }
-}
-
-// Eight 16-bit row elements (one 16-byte piece) of a 128-wide row spread over
-// 16 consecutive lanes: for kRaw != 0 the row is L2-normalised, x rsqrt(sum
-// x^2 + 1e-6) in fp32 and rounded to bf16 (the reference adapter's
-// normalisation, gdnChunkPrefillSm87.cu:52-84; transformers l2norm,
-// modeling_qwen3_5.py:242-245); the result is returned as fp16, which holds
-// every such bf16 value exactly in fp16's normal range.
-template <int kRaw>
-__device__ inline half8 row_piece_to_half8(u32x4 w) {
-    float x[8];
+__device__ inline void unpack8(u32x4 w, float (&x)[8]) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         x[2 * p] = raw16<kRaw>(w[p] & 0xffffu);
         x[2 * p + 1] = raw16<kRaw>(w[p] >> 16);
     }
-    if constexpr (kRaw != 0) {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
-        const float inv = rsqrtf(ss + 1e-6f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (float)(__bf16)(x[e] * inv);
-    }
+}
+
+__device__ inline half8 f32x8_to_half8(const float (&x)[8]) {
     half8 h;
 #pragma unroll
     for (int e = 0; e < 8; ++e) h[e] = (_Float16)x[e];
     return h;
+}
+
+__device__ inline u32x4 f32x8_to_bf16x8(const float (&x)[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+        w[p] = (uint32_t)f32_to_bf16_bits(x[2 * p]) | ((uint32_t)f32_to_bf16_bits(x[2 * p + 1]) << 16);
+    return w;
 }
 
 __device__ __forceinline__ f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
@@ -196,7 +214,37 @@ __device__ __forceinline__ s16x4 lds_read_tr(const void* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
 }
 
-__device__ __forceinline__ half4 s16x4_as_half4(s16x4 v) { return __builtin_bit_cast(half4, v); }
+__device__ __forceinline__ half8 tr_pair_half8(s16x4 lo, s16x4 hi) {
+    return cat8(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi));
+}
+
+__device__ __forceinline__ bf16x8 tr_pair_bf16x8(s16x4 lo, s16x4 hi) {
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    s16x8 r;
+    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// Row pieces of a 64 x 128 16-bit tile in LDS: piece p (8 elements) of row r
+// sits at 16 r + (p ^ (r & 15)), so both 16-byte row-piece reads and the
+// transposing reads below are free of bank conflicts.
+__device__ __forceinline__ int row_slot(int r, int p) { return 16 * r + (p ^ (r & 15)); }
+
+// Transposed operand of rows tile t (0..7) and token k-block kb (0..1) of a
+// 64-token tile stored as above: lane (g, m) receives rows
+// dk(t, m) = 32 (t / 2) + 8 (m / 4) + 4 (t % 2) + m % 4 for the 8 tokens
+// 32 kb + kmap(g, j).  A product with this as its A operand yields D tiles
+// whose lane (g, n), element i is dk 32 (t / 2) + 8 g + 4 (t % 2) + i: two
+// tiles 2p, 2p+1 hold dk 32 p + 8 g + 0..7 in order.
+__device__ __forceinline__ void kt_reads(const uint16_t* base, int t, int kb, int lane, s16x4& x0,
+                                         s16x4& x1) {
+    const int lg = lane >> 4, lm = lane & 15;
+    const int p = 4 * (t >> 1) + (lm & 3);
+    const int r0 = 32 * kb + 4 * lg + (lm >> 2), r1 = r0 + 16;
+    x0 = lds_read_tr(base + row_slot(r0, p) * 8 + 4 * (t & 1));
+    x1 = lds_read_tr(base + row_slot(r1, p) * 8 + 4 * (t & 1));
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -282,11 +330,10 @@ __device__ bool locate_chunk(const int32_t* cu, int N, int T, int total, int cid
 // ---------------------------------------------------------------------------
 // prep kernel: one work-group (4 waves) per (chunk, v-head)
 // ---------------------------------------------------------------------------
-constexpr int kKS = kDK + 8;      // bf16 K row pitch: 136 halves (272 B, 16-byte aligned)
 constexpr int kMS = kChunk + 4;   // fp32 A / T row pitch: 68 floats
 
 struct PrepSmem {
-    uint16_t Kr[kChunk * kKS];   // K rows (bf16), [token][dk]
+    u32x4 K[kChunk * 16];   // fp16 K rows, row_slot layout
     // A (strictly lower, row-major) on entry.  The inverse overwrites it in
     // place: diagonal blocks T_ii row-major at (i, i); T_ij (i > j) stored
     // transposed at block (j, i), where A is zero and never read.  Its first
@@ -307,17 +354,11 @@ __device__ inline f32x4 t_row4(const float* AT, int rb, int cb, int r, int c0) {
     return t;
 }
 
-// Two 4-element bf16 pieces (k-map registers 0..3 and 4..7) as one operand
-__device__ inline bf16x8 bf16_frag(uint2 lo, uint2 hi) {
-    const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
-    return __builtin_bit_cast(bf16x8, w);
-}
-
 // K K^T and K Q^T products of wave W: A column block W (row tiles W..3) and
 // M^T column block W (row tiles 0..W), k-blocks outermost so the five
-// accumulators' products interleave.
+// accumulators' products interleave.  Every operand holds 8 consecutive dk.
 template <int W>
-__device__ inline void am_products(const bf16x8 (&ka)[4][4], const bf16x8 (&qf)[4],
+__device__ inline void am_products(const half8 (&ka)[4][4], const half8 (&qf)[4],
                                    f32x4 (&accA)[4], f32x4 (&accM)[4]) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -327,23 +368,10 @@ __device__ inline void am_products(const bf16x8 (&ka)[4][4], const bf16x8 (&qf)[
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-        for (int mt = W; mt < 4; ++mt) accA[mt] = mfma16_bf16(ka[mt][kb], ka[W][kb], accA[mt]);
+        for (int mt = W; mt < 4; ++mt) accA[mt] = mfma16(ka[mt][kb], ka[W][kb], accA[mt]);
 #pragma unroll
-        for (int mt = 0; mt <= W; ++mt) accM[mt] = mfma16_bf16(ka[mt][kb], qf[kb], accM[mt]);
+        for (int mt = 0; mt <= W; ++mt) accM[mt] = mfma16(ka[mt][kb], qf[kb], accM[mt]);
     }
-}
-
-// bf16 pair of a raw 16-bit pair, L2-scaled by inv (kRaw != 0)
-template <int kRaw>
-__device__ inline uint32_t norm_pair(uint32_t w, float inv) {
-    const float lo = raw16<kRaw>(w & 0xffffu) * inv, hi = raw16<kRaw>(w >> 16) * inv;
-    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
-}
-
-template <int kRaw>
-__device__ inline float sumsq_pair(uint32_t w, float s) {
-    const float lo = raw16<kRaw>(w & 0xffffu), hi = raw16<kRaw>(w >> 16);
-    return fmaf(hi, hi, fmaf(lo, lo, s));
 }
 
 template <bool kDbg, int kRaw>
@@ -369,7 +397,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     const int z = (rest / rep) * 8 + (L & 7);
     const int cid = z / HK, hk = z - cid * HK;
     if (cid >= nch_bound) return;
-    const int hv = hk * rep + (rest % rep);
+    const int member = rest % rep;
+    const int hv = hk * rep + member;
 
     int seq, tok0, rows;
     if (!locate_chunk<kPrepThreads>(cu, N, T, total, cid, reinterpret_cast<int*>(sm.AT), seq,
@@ -396,6 +425,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             gdt = in.dt_bias[hv];
         }
     }
+    // K: thread tid holds piece tid % 16 of rows tid / 16 + 16 ii
     u32x4 raw[4];
     {
         const uint16_t* base = k + ((size_t)tok0 * HK + hk) * kDK + 8 * (tid & 15);
@@ -405,15 +435,13 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             raw[ii] = *reinterpret_cast<const u32x4*>(base + (size_t)r * HK * kDK);
         }
     }
-    uint2 qr[4][2];
+    // Q: wave w, lane (lg, lm) holds row 16 w + lm, dk 32 kb + 8 lg .. + 7
+    u32x4 qr[4];
     {
         const uint16_t* qs =
-            q + ((size_t)(tok0 + min(wave * 16 + lm, rows - 1)) * HK + hk) * kDK + 4 * lg;
+            q + ((size_t)(tok0 + min(wave * 16 + lm, rows - 1)) * HK + hk) * kDK + 8 * lg;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            qr[kb][0] = *reinterpret_cast<const uint2*>(qs + kb * 32);
-            qr[kb][1] = *reinterpret_cast<const uint2*>(qs + kb * 32 + 16);
-        }
+        for (int kb = 0; kb < 4; ++kb) qr[kb] = *reinterpret_cast<const u32x4*>(qs + kb * 32);
     }
     // the gate arithmetic (and so the wait for its inputs) stays behind the
     // K and Q loads
@@ -427,45 +455,71 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         }
     }
 
-    if constexpr (kRaw != 0) {
-        // raw inputs: K rows (16 lanes per row, 8 values each) and Q rows (4
-        // lanes per row, 32 values each) L2-normalised and rounded to bf16
+    // ---- K rows -> fp16 into LDS (normalised first for raw inputs); rows
+    // past the chunk's end are zeroed.  For raw inputs the first v-head of
+    // the GQA group also stores the normalised bf16 rows for the scan.
+    const bool writer = member == 0;
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
+    for (int ii = 0; ii < 4; ++ii) {
+        const int r = (tid >> 4) + 16 * ii, p = tid & 15;
+        float x[8];
+        unpack8<kRaw>(raw[ii], x);
+        if constexpr (kRaw != 0) {
             float ss = 0.f;
 #pragma unroll
-            for (int p = 0; p < 4; ++p) ss = sumsq_pair<kRaw>(raw[ii][p], ss);
+            for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
 #pragma unroll
             for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
             const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
-            for (int p = 0; p < 4; ++p) raw[ii][p] = norm_pair<kRaw>(raw[ii][p], inv);
+            for (int e = 0; e < 8; ++e) x[e] = (float)(__bf16)(x[e] * inv);
+            if (writer && r < rows)
+                *reinterpret_cast<u32x4*>(ws.Kn + ((size_t)(tok0 + r) * HK + hk) * kDK + 8 * p) =
+                    f32x8_to_bf16x8(x);
         }
-        {
-            float ss = 0.f;
+        u32x4 v = __builtin_bit_cast(u32x4, f32x8_to_half8(x));
+        if (r >= rows) v = u32x4{0u, 0u, 0u, 0u};
+        sm.K[row_slot(r, p)] = v;
+    }
+    // ---- Q row pieces -> fp16 (normalised first for raw inputs: a row's 128
+    // values are spread over the 4 lanes lm, lm + 16, lm + 32, lm + 48)
+    half8 qf[4];
+    {
+        float x[4][8];
+        float ss = 0.f;
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < 4; ++kb) {
+            unpack8<kRaw>(qr[kb], x[kb]);
 #pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
-                    ss = sumsq_pair<kRaw>(qr[kb][h2].x, ss);
-                    ss = sumsq_pair<kRaw>(qr[kb][h2].y, ss);
-                }
-            }
+            for (int e = 0; e < 8; ++e) ss = fmaf(x[kb][e], x[kb][e], ss);
+        }
+        if constexpr (kRaw != 0) {
             ss += __shfl_xor(ss, 16, 64);
             ss += __shfl_xor(ss, 32, 64);
             const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
-                    qr[kb][h2].x = norm_pair<kRaw>(qr[kb][h2].x, inv);
-                    qr[kb][h2].y = norm_pair<kRaw>(qr[kb][h2].y, inv);
-                }
+                for (int e = 0; e < 8; ++e) x[kb][e] = (float)(__bf16)(x[kb][e] * inv);
             }
+        }
+        const bool ok = wave * 16 + lm < rows;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            qf[kb] = f32x8_to_half8(x[kb]);
+            if (!ok) qf[kb] = half8{};
+        }
+        // Q fragments for the scan's output wave: fragment (mt = wave, kb)
+        if (writer) {
+            half8* qdst = ws.Q + ((size_t)cid * HK + hk) * 16 * 64;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) qdst[(wave * 4 + kb) * 64 + lane] = qf[kb];
         }
     }
 
-    // ---- gates (wave 0): c = cumsum(g); padded rows have g = beta = 0
+    // ---- gates (wave 0): c = cumsum(g); padded rows have g = beta = 0.  The
+    // gates record holds beta, d = e^{c63 - c} (0 on padded rows), s e^c and
+    // c63.
     if (wave == 0) {
         if (lane >= rows) {
             gv = 0.f;
@@ -477,17 +531,15 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             const float o = __shfl_up(cs, off, 64);
             if (lane >= off) cs += o;
         }
+        const float c63 = __shfl(cs, 63, 64);
         sm.cl[lane] = cs * kLog2e;
         sm.b[lane] = bv;
+        float* gr = ws.gates + ch * (kGateBytes / 4);
+        gr[kGBeta + lane] = bv;
+        gr[kGDec + lane] = lane < rows ? __builtin_amdgcn_exp2f((c63 - cs) * kLog2e) : 0.f;
+        gr[kGSec + lane] = scale * __builtin_amdgcn_exp2f(cs * kLog2e);
+        gr[kGC63 + lane] = lane == 0 ? c63 : 0.f;
         if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
-    }
-
-    // ---- K rows -> LDS as loaded; rows past the chunk's end are zeroed
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-        const int r = (tid >> 4) + 16 * ii;
-        const uint32_t m = r < rows ? 0xffffffffu : 0u;
-        *reinterpret_cast<u32x4*>(&sm.Kr[r * kKS + 8 * (tid & 15)]) = raw[ii] & m;
     }
     __syncthreads();
 
@@ -496,21 +548,13 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     // r in [16w, 16w+16) of M (computed as M^T = K Q^T, whose accumulators are
     // already the M fragments the scan reads).
     {
-        const uint2 z2 = {0u, 0u};
-        bf16x8 ka[4][4], qf[4];
+        half8 ka[4][4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            const uint16_t* src = &sm.Kr[(mt * 16 + lm) * kKS + 4 * lg];
+            const int r = mt * 16 + lm;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
-                ka[mt][kb] = bf16_frag(*reinterpret_cast<const uint2*>(src + kb * 32),
-                                       *reinterpret_cast<const uint2*>(src + kb * 32 + 16));
-        }
-        {
-            const bool ok = wave * 16 + lm < rows;
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-                qf[kb] = bf16_frag(ok ? qr[kb][0] : z2, ok ? qr[kb][1] : z2);
+                ka[mt][kb] = __builtin_bit_cast(half8, sm.K[row_slot(r, 4 * kb + lg)]);
         }
         f32x4 accA[4], accM[4];
         switch (wave) {
@@ -649,12 +693,14 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         }
     }
 
-    // ---- (T - I) fragments: wave w writes row tile mt = w, k-blocks
-    // kb <= mt / 2; lane (lg, lm) holds T[16mt + lm][32kb + kmap(lg, j)]
+    // ---- (T - I) fragments as an fp16 hi / lo pair: wave w writes row tile
+    // mt = w, k-blocks kb <= mt / 2; lane (lg, lm) holds T[16mt + lm][32kb +
+    // kmap(lg, j)]
     {
         const int mt = wave;
         const int r = mt * 16 + lm;
         half8* tdst = ws.TI + ch * (kTri * 64);
+        half8* ldst = ws.TIlo + ch * (kTri * 64);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             if (kb > mt / 2) break;
@@ -666,67 +712,113 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                 if (c0 + e == r) t0[e] -= 1.f;
                 if (c0 + 16 + e == r) t1[e] -= 1.f;
             }
-            tdst[(tri_base(mt) + kb) * 64 + lane] = cat8(to_half4(t0), to_half4(t1));
+            const half4 h0 = to_half4(t0), h1 = to_half4(t1);
+            f32x4 l0, l1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                l0[e] = t0[e] - (float)h0[e];
+                l1[e] = t1[e] - (float)h1[e];
+            }
+            tdst[(tri_base(mt) + kb) * 64 + lane] = cat8(h0, h1);
+            ldst[(tri_base(mt) + kb) * 64 + lane] = cat8(to_half4(l0), to_half4(l1));
+        }
+    }
+
+    // ---- -W = -T diag(beta e^c) K as W^T = K^T (T diag(beta e^c))^T: wave w
+    // forms dk tiles t = 2w, 2w+1 (dk 32 w .. 32 w + 31) for every token tile
+    // mt.  The A operand is K^T from the transposing reads; the B operand of
+    // (k-block kb, token tile mt) holds T[16 mt + n][32 kb + kmap(g, j)]
+    // beta_j e^{c_j}, rounded once to fp16.  Lane (g, n) then holds -W[16 mt
+    // + n][32 w + 8 g + 0..7]: fragment (mt, kb = w) of the scan's A operand.
+    {
+        const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sm.K);
+        half8 kt[2][2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                s16x4 x0, x1;
+                kt_reads(kbase, 2 * wave + tt, kb, lane, x0, x1);
+                kt[tt][kb] = tr_pair_half8(x0, x1);
+            }
+        }
+        f32x4 bec[2][2];   // beta e^c at columns 32 kb + 4 g (+16) .. + 3
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int c0 = 32 * kb + 16 * hh + 4 * lg;
+                const f32x4 bb = *reinterpret_cast<const f32x4*>(&sm.b[c0]);
+                const f32x4 cc = *reinterpret_cast<const f32x4*>(&sm.cl[c0]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bec[kb][hh][e] = bb[e] * __builtin_amdgcn_exp2f(cc[e]);
+            }
+        }
+        half8* wdst = ws.W + ch * (16 * 64);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int r = 16 * mt + lm;
+            f32x4 acc0 = zero4(), acc1 = zero4();
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                if (kb > mt / 2) break;
+                f32x4 t0 = t_row4(sm.AT, mt, 2 * kb, r, 32 * kb + 4 * lg);
+                f32x4 t1 = t_row4(sm.AT, mt, 2 * kb + 1, r, 32 * kb + 16 + 4 * lg);
+                const half8 bt = cat8(to_half4(t0 * bec[kb][0]), to_half4(t1 * bec[kb][1]));
+                acc0 = mfma16(kt[0][kb], bt, acc0);
+                acc1 = mfma16(kt[1][kb], bt, acc1);
+            }
+            wdst[(mt * 4 + wave) * 64 + lane] = cat8(to_half4(-acc0), to_half4(-acc1));
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (8 waves) per (32 value columns, v-head,
-// sequence).  The 32 columns form two 16-column slices, interleaved in
-// groups of four: slice h holds columns 32 pr + 8 (n / 4) + 4 h + n % 4 for
-// MFMA column n, so the output wave's two D tiles of one token are 8
-// consecutive columns (one 16-byte store).
+// scan kernel: one work-group (4 waves, one per SIMD) per (16 value columns,
+// v-head, sequence).
 //
-// State layout of a chain wave: accumulator tile t (0..7), lane (g, n),
-// element i holds S[dk][col(n)] with dk = 32 (t/2) + 8 g + 4 (t%2) + i.  Then
-// the fp16 B operand of k-block kb (tiles 2kb, 2kb+1) holds dk 32 kb + 8 g +
-// 0..7 in order, matching 16-byte reads of K and Q rows, and the K^T operand
-// producing tile t is two transposing LDS reads.
+// State layout of the chain: accumulator tile t (0..7), lane (g, n), element
+// i holds S[dk][16 sl + n] with dk = 32 (t/2) + 8 g + 4 (t%2) + i, so the
+// fp16 B operand of k-block kb (tiles 2kb, 2kb+1) holds dk 32 kb + 8 g + 0..7
+// in order, matching the -W row-piece fragments, and the K^T operand that
+// produces tile t is two transposing LDS reads of K rows.
 //
-//   chains   wave h (h = 0, 1) on SIMD h: P = K S (16 MFMA), R (VALU),
-//            V_n = R + (T - I) R (6), S' = e^{c63} S + K^T (d V_n)_hi (16),
-//            Sc' = e^{c63} Sc + K^T (d V_n)_lo (16, off the serial path).
-//   output   wave 2: O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T for both slices.
-//   loaders  wave 3: K rows -> fp16, gates -> ring A; wave 7: Q rows ->
-//            fp16, s e^c -> ring B; wave 6: V rows and T - I -> ring A, M ->
-//            ring B, as direct-to-LDS loads.  Waves 4 and 5 exit at once, so
-//            each chain has its SIMD to itself.
+//   chain     wave 0: V_n = U + (-W) S16 (16 fp16 MFMA), d V_n -> bf16 hi / lo,
+//             S' = e^{c63} S + K^T hi (16 bf16 MFMA), Sc += K^T (sigma lo)
+//             (16 bf16 MFMA, off the serial path: sigma = e^{sum of the
+//             later chunks' c63} pre-applies the decay the lo part would
+//             see, so Sc needs no per-chunk scaling).
+//   producer  wave 1: U = beta V + (T - I)(beta V) with the product as
+//             hi/hi + hi/lo + lo/hi fp16 MFMAs (18), into ring A.
+//   output    wave 2: O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T, with Q, M and
+//             s e^c loaded to registers one chunk ahead.
+//   loader    wave 3: K rows, -W, V and the gates record into ring A as
+//             direct-to-LDS loads.
 // ---------------------------------------------------------------------------
 constexpr int kRingA = 3;     // chain operand stages
-constexpr int kRingB = 2;     // output operand stages
 constexpr int kHand = 2;      // chain -> output hand-off slots
 
 struct StageA {
-    u32x4 K[kChunk * 16];   // fp16 K rows; piece p of row r at 16 r + (p ^ (r & 15))
-    u32x4 V[kChunk * 4];    // raw 16-bit V rows of the pair's 32 columns, 4 pieces per row
-    half8 TI[kTri][64];     // (T - I) fragments
-    float beta[kChunk], bec[kChunk], dec[kChunk];   // beta, beta e^c, e^{c63 - c}
-    float gam;                                      // e^{c63}
-    float pad_[3];
-};
-
-struct StageB {
-    u32x4 Q[kChunk * 16];   // fp16 Q rows, same swizzle as K
-    half8 M[kTri][64];      // M fragments
-    float sec[kChunk];      // s e^c
+    u32x4 K[kChunk * 16];   // bf16 K rows, row_slot layout
+    half8 W[16][64];        // -W fragments (mt * 4 + kb)
+    f32x4 U[4][64];         // U, D layout per row tile (producer)
+    u32x4 V[kChunk * 2];    // V rows of the slice's 16 columns, 2 pieces per row
+    float gates[256];       // gates record
 };
 
 struct Hand {
-    half8 S[2][4][64];      // S at the chunk's start, fp16 B fragments per slice
-    half8 V[2][2][64];      // V_n, fp16 B fragments per slice
+    half8 S[4][64];         // S at the chunk's start, fp16 B fragments
+    half8 V[2][64];         // V_n, fp16 B fragments
 };
 
 struct ScanSmem {
     StageA a[kRingA];
-    StageB b[kRingB];
     Hand h[kHand];
-    int fillA[2];    // chunks in ring A: 0 K loader, 1 aux loader
-    int fillB[2];    // chunks in ring B: 0 Q loader, 1 aux loader
-    int freeA[2];    // per chain: chunks whose ring-A stage it has finished reading
-    int freeB;       // output: chunks whose ring-B stage it has finished reading
-    int ready[2];    // per chain: chunks whose hand-off part is written
-    int cons;        // output: chunks whose hand-off slot it has read
+    int fillA;       // chunks whose ring-A loads have landed (loader)
+    int uready;      // chunks whose U is in ring A (producer)
+    int freeA;       // chunks whose ring-A stage the chain has finished reading
+    int ready;       // chunks whose hand-off slot the chain has written
+    int cons;        // chunks whose hand-off slot the output has read
     int abort;       // a bounded wait ran out: every wave stops
     int seqsel;
     int red[kScanThreads / 64];
@@ -783,148 +875,85 @@ struct ScanArgs {
     const float* s0;
     float* sf;
     const int32_t* cu;
+    const uint16_t* krows;   // K rows for the state update: the input k, or the normalised Kn
     int N, T, total, HV, HK, nch_bound;
     unsigned spin;
 };
 
-// Loader of K (kQ = false, ring A, with the chains' gates) or Q (kQ = true,
-// ring B, with s e^c) rows: 16 pieces of 16 bytes per lane per chunk, two
-// chunks in flight; rows become fp16 (normalised first for raw inputs) and
-// are written with the row swizzle.  Rows past the chunk's end are zero.
-template <bool kQ, int kRaw>
-__device__ void run_row_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, int hk, int hv,
-                               int tok_base, int len, int nch, float scale, int lane) {
-    const uint16_t* __restrict__ src = kQ ? a.in.q : a.in.k;
-    struct Buf {
-        u32x4 r[16];
-        float g, b;
-    };
-    auto load = [&](int c, Buf& f) {
-        const int cc = min(c, nch - 1);
-        const int t0 = tok_base + cc * kChunk, rows = min(kChunk, len - cc * kChunk);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = min(4 * i + (lane >> 4), rows - 1);
-            f.r[i] = *reinterpret_cast<const u32x4*>(src + ((size_t)(t0 + r) * a.HK + hk) * kDK +
-                                                      8 * (lane & 15));
-        }
-        load_gate<kRaw>(a.in, (size_t)(t0 + min(lane, rows - 1)) * a.HV + hv, hv, f.g, f.b);
-    };
-    auto store = [&](int c, const Buf& f) -> bool {
-        const bool ok = kQ ? w.until([&] { return lds_ld(&sm.freeB) >= c - kRingB + 1; })
-                           : w.until([&] {
-                                 return min(lds_ld(&sm.freeA[0]), lds_ld(&sm.freeA[1])) >=
-                                        c - kRingA + 1;
-                             });
-        if (!ok) return false;
-        asm volatile("" ::: "memory");
-        const int rows = min(kChunk, len - c * kChunk);
-        u32x4* dst = kQ ? sm.b[c % kRingB].Q : sm.a[c % kRingA].K;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = 4 * i + (lane >> 4), p = lane & 15;
-            half8 h = row_piece_to_half8<kRaw>(f.r[i]);
-            u32x4 v = __builtin_bit_cast(u32x4, h);
-            if (r >= rows) v = u32x4{0u, 0u, 0u, 0u};
-            dst[16 * r + (p ^ (r & 15))] = v;
-        }
-        // gates: c = cumsum(g) over the chunk (padded rows g = beta = 0)
-        const float gv = lane < rows ? f.g : 0.f, bv = lane < rows ? f.b : 0.f;
-        float cs = gv;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float o = __shfl_up(cs, off, 64);
-            if (lane >= off) cs += o;
-        }
-        const float clast = __shfl(cs, 63, 64);
-        const float ec = exp2f(cs * kLog2e);
-        if constexpr (kQ) {
-            sm.b[c % kRingB].sec[lane] = scale * ec;
-        } else {
-            StageA& st = sm.a[c % kRingA];
-            st.beta[lane] = bv;
-            st.bec[lane] = bv * ec;
-            st.dec[lane] = exp2f((clast - cs) * kLog2e);
-            if (lane == 0) st.gam = exp2f(clast * kLog2e);
-        }
-        lds_wait_all();
-        if (lane == 0) lds_st(kQ ? &sm.fillB[0] : &sm.fillA[0], c + 1);
-        return true;
-    };
-    if (nch <= 0) return;
-    Buf fa, fb;
-    load(0, fa);
-    for (int c = 0; c < nch; c += 2) {
-        load(c + 1, fb);
-        if (!store(c, fa)) return;
-        if (c + 1 >= nch) return;
-        load(c + 2, fa);
-        if (!store(c + 1, fb)) return;
-    }
+struct ScanCtx {
+    int seq, hv, hk, sl, tok_base, len, chunk0, nch;
+};
+
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
-// Direct-to-LDS loader of V (the pair's 32 columns), T - I (ring A) and M
-// (ring B).  A chunk's 16 loads go out as soon as its stages are free; its
-// counters are set once the loads of the next chunk are issued and its own
-// have landed.
-__device__ void run_aux_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, int hv, int pr,
-                               int tok_base, int len, int chunk0, int nch, int lane) {
-    auto issue = [&](int c) -> bool {
-        const bool ok = w.until([&] {
-            return min(lds_ld(&sm.freeA[0]), lds_ld(&sm.freeA[1])) >= c - kRingA + 1 &&
-                   lds_ld(&sm.freeB) >= c - kRingB + 1;
-        });
-        if (!ok) return false;
+// Loader: 35 direct-to-LDS loads per chunk (16 for K rows, 16 for -W, 2 for
+// V, 1 for the gates).  A chunk's loads go out as soon as its stage is free;
+// its counter is set as soon as they have landed.  The next chunk's loads are
+// issued first when its stage is already free, so two chunks can be in
+// flight.
+constexpr int kLoadsPerChunk = 35;
+// s_waitcnt immediates: vmcnt(n) with expcnt and lgkmcnt left at their
+// maxima; vmcnt's 6 bits are split over bits 3:0 and 15:14
+constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
+constexpr unsigned kVmcntOneChunk = vmcnt_imm(kLoadsPerChunk);
+constexpr unsigned kVmcntBeforeNext = vmcnt_imm(63 - kLoadsPerChunk);
+static_assert(vmcnt_imm(16) == 0x4F70 && vmcnt_imm(0) == 0x0F70, "s_waitcnt encoding");
+
+__device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                           int lane) {
+    auto stage_free = [&](int c) { return lds_ld(&sm.freeA) >= c - kRingA + 1; };
+    auto issue = [&](int c) {
         asm volatile("" ::: "memory");
-        StageA& sa = sm.a[c % kRingA];
-        StageB& sb = sm.b[c % kRingB];
-        const int t0 = tok_base + c * kChunk, rows = min(kChunk, len - c * kChunk);
-        // V: slot 64 i + lane = row (16 i + lane / 4), piece lane % 4
+        StageA& st = sm.a[c % kRingA];
+        const int t0 = x.tok_base + c * kChunk, rows = min(kChunk, x.len - c * kChunk);
+        const size_t ch = (size_t)(x.chunk0 + c) * a.HV + x.hv;
+        // K rows: slot s = 64 i + lane -> row s / 16, stored piece s % 16,
+        // which is source piece (s % 16) ^ (row % 16)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = min(16 * i + (lane >> 2), rows - 1);
-            const uint16_t* gp =
-                a.in.v + ((size_t)(t0 + r) * a.HV + hv) * kDV + kPairCols * pr + 8 * (lane & 3);
-            __builtin_amdgcn_global_load_lds(gp, (__attribute__((address_space(3))) void*)&sa.V[64 * i],
-                                             16, 0, 0);
+        for (int i = 0; i < 16; ++i) {
+            const int s = 64 * i + lane, r = s >> 4, p = (s & 15) ^ (r & 15);
+            const int rr = min(r, rows - 1);
+            lds_dma16(a.krows + ((size_t)(t0 + rr) * a.HK + x.hk) * kDK + 8 * p, &st.K[64 * i]);
         }
-        const size_t ch = (size_t)(chunk0 + c) * a.HV + hv;
-        const half8* ti = a.ws.TI + ch * (kTri * 64) + lane;
-        const half8* mm = a.ws.M + ch * (kTri * 64) + lane;
+        const half8* wsrc = a.ws.W + ch * (16 * 64) + lane;
 #pragma unroll
-        for (int f = 0; f < kTri; ++f)
-            __builtin_amdgcn_global_load_lds(ti + f * 64, (__attribute__((address_space(3))) void*)&sa.TI[f][0],
-                                             16, 0, 0);
+        for (int f = 0; f < 16; ++f) lds_dma16(wsrc + f * 64, &st.W[f][0]);
+        // V: slot 64 i + lane -> row (64 i + lane) / 2, piece lane % 2
 #pragma unroll
-        for (int f = 0; f < kTri; ++f)
-            __builtin_amdgcn_global_load_lds(mm + f * 64, (__attribute__((address_space(3))) void*)&sb.M[f][0],
-                                             16, 0, 0);
-        return true;
+        for (int i = 0; i < 2; ++i) {
+            const int s = 64 * i + lane, r = min(s >> 1, rows - 1);
+            lds_dma16(a.in.v + ((size_t)(t0 + r) * a.HV + x.hv) * kDV + kSliceCols * x.sl + 8 * (s & 1),
+                      &st.V[64 * i]);
+        }
+        lds_dma16(a.ws.gates + ch * (kGateBytes / 4) + 4 * lane, &st.gates[0]);
     };
-    auto publish = [&](int c) {
-        if (lane == 0) {
-            lds_st(&sm.fillA[1], c + 1);
-            lds_st(&sm.fillB[1], c + 1);
-        }
-    };
-    for (int c = 0; c < nch; ++c) {
-        if (!issue(c)) {
-            vm_wait_all();   // no load may land in LDS after the group ends
-            return;
-        }
-        if (c > 0) {
-            // the previous chunk's 16 loads have landed (this chunk's 16 may
-            // still be in flight): vmcnt(16)
+    if (x.nch <= 0) return;
+    issue(0);   // stage 0 starts free
+    for (int c = 0; c < x.nch; ++c) {
+        const bool more = c + 1 < x.nch;
+        const bool ahead = more && stage_free(c + 1);
+        if (ahead) {
+            // at most 63 loads outstanding (the counter's range): let chunk
+            // c drain to 63 - 35 before chunk c + 1 goes out
             asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_waitcnt(0x4F70);
+            __builtin_amdgcn_s_waitcnt(kVmcntBeforeNext);
+            issue(c + 1);
+            // chunk c's loads have landed, chunk c + 1's may be in flight
             asm volatile("" ::: "memory");
-            publish(c - 1);
+            __builtin_amdgcn_s_waitcnt(kVmcntOneChunk);
+            asm volatile("" ::: "memory");
+        } else {
+            vm_wait_all();
+        }
+        if (lane == 0) lds_st(&sm.fillA, c + 1);
+        if (more && !ahead) {
+            if (!w.until([&] { return stage_free(c + 1); })) return;   // nothing in flight
+            issue(c + 1);
         }
     }
-    if (nch > 0) {
-        vm_wait_all();
-        publish(nch - 1);
-    }
+    vm_wait_all();
 }
 
 template <int kRaw>
@@ -934,16 +963,98 @@ __device__ inline float v16_to_f32(uint32_t bits) {
     return __uint_as_float(bits << 16);
 }
 
-template <int kRaw, bool kDbg>
-__device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, int h, int seq, int hv,
-                          int pr, int chunk0, int nch, int lane) {
+// Producer: U = beta V + (T - I)(beta V) per chunk into ring A.  With X =
+// beta V (fp32, D layout), the product is (T-I)_hi X_hi + (T-I)_hi X_lo +
+// (T-I)_lo X_hi on fp16 MFMA, accumulated onto X.
+template <int kRaw>
+__device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                             int lane) {
     const int lg = lane >> 4, lm = lane & 15;
-    // column of MFMA column lm in this slice, and dk of (tile t, element i)
-    const int col = kPairCols * pr + 8 * (lm >> 2) + 4 * h + (lm & 3);
-    auto dk_of = [&](int t, int i) { return 32 * (t >> 1) + 8 * lg + 4 * (t & 1) + i; };
-    const size_t sbase = ((size_t)seq * a.HV + hv) * kDK * kDV + col;
+    half8 th[kTri], tl[kTri], nh[kTri], nl[kTri];
+    auto load_t = [&](int c, half8 (&h)[kTri], half8 (&l)[kTri]) {
+        const int cc = min(c, x.nch - 1);
+        const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
+        const half8* ph = a.ws.TI + ch * (kTri * 64) + lane;
+        const half8* pl = a.ws.TIlo + ch * (kTri * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < kTri; ++f) {
+            h[f] = ph[f * 64];
+            l[f] = pl[f * 64];
+        }
+    };
+    if (x.nch <= 0) return;
+    load_t(0, th, tl);
+    for (int c = 0; c < x.nch; ++c) {
+        load_t(c + 1, nh, nl);
+        if (!w.until([&] { return lds_ld(&sm.fillA) >= c + 1; })) return;
+        asm volatile("" ::: "memory");
+        StageA& st = sm.a[c % kRingA];
+        // X = beta V: lane (g, n) of tile mt holds tokens 16 mt + 4 g + i of
+        // column n (transposing read: source lane (a4 = lm / 4, b4 = lm % 4)
+        // names row 16 mt + 4 lg + a4, columns 4 b4 .. + 3)
+        f32x4 X[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const f32x4 be = *reinterpret_cast<const f32x4*>(&st.gates[kGBeta + 16 * mt + 4 * lg]);
+            const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(st.V) +
+                                   (16 * mt + 4 * lg + (lm >> 2)) * kSliceCols + 4 * (lm & 3);
+            const s16x4 vt = lds_read_tr(vsrc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) X[mt][i] = be[i] * v16_to_f32<kRaw>((uint16_t)vt[i]);
+        }
+        half8 xh[2], xl[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const half4 h0 = to_half4(X[2 * kb]), h1 = to_half4(X[2 * kb + 1]);
+            f32x4 r0, r1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                r0[i] = X[2 * kb][i] - (float)h0[i];
+                r1[i] = X[2 * kb + 1][i] - (float)h1[i];
+            }
+            xh[kb] = cat8(h0, h1);
+            xl[kb] = cat8(to_half4(r0), to_half4(r1));
+        }
+        f32x4 U[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            U[mt] = X[mt];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                if (kb > mt / 2) break;
+                const int f = tri_base(mt) + kb;
+                U[mt] = mfma16(th[f], xh[kb], U[mt]);
+                U[mt] = mfma16(th[f], xl[kb], U[mt]);
+                U[mt] = mfma16(tl[f], xh[kb], U[mt]);
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) st.U[mt][lane] = U[mt];
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.uready, c + 1);
+#pragma unroll
+        for (int f = 0; f < kTri; ++f) {
+            th[f] = nh[f];
+            tl[f] = nl[f];
+        }
+    }
+}
 
-    f32x4 S[8], Sc[8];
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+template <bool kDbg>
+__device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                          int lane) {
+    const int lg = lane >> 4, lm = lane & 15;
+    const int col = kSliceCols * x.sl + lm;
+    auto dk_of = [&](int t, int i) { return 32 * (t >> 1) + 8 * lg + 4 * (t & 1) + i; };
+    const size_t sbase = ((size_t)x.seq * a.HV + x.hv) * kDK * kDV + col;
+
+    // Sd (debug builds only): the lo part without the sigma pre-scaling,
+    // decayed every chunk, so S + Sd is the state at each chunk's start
+    f32x4 S[8], Sc[8], Sd[8];
     if (a.s0) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -955,132 +1066,137 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, int 
         for (int t = 0; t < 8; ++t) S[t] = zero4();
     }
 #pragma unroll
-    for (int t = 0; t < 8; ++t) Sc[t] = zero4();
+    for (int t = 0; t < 8; ++t) {
+        Sc[t] = zero4();
+        Sd[t] = zero4();
+    }
+
+    // remaining log-decay after each chunk: rem = sum of c63 over the later
+    // chunks of this sequence; starts as the total
+    float rem = 0.f;
+    {
+        for (int j0 = 0; j0 < x.nch; j0 += 64) {
+            const int j = j0 + lane;
+            float v = 0.f;
+            if (j < x.nch) v = a.ws.gates[((size_t)(x.chunk0 + j) * a.HV + x.hv) * (kGateBytes / 4) + kGC63];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            rem += v;
+        }
+    }
+
     half8 S16[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) S16[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
 
     bool ok = true;
-    for (int c = 0; c < nch; ++c) {
+    for (int c = 0; c < x.nch; ++c) {
         const int st = c % kRingA, hs = c % kHand;
         ok = w.until([&] {
-            return min(lds_ld(&sm.fillA[0]), lds_ld(&sm.fillA[1])) >= c + 1 &&
-                   lds_ld(&sm.cons) >= c - kHand + 1;
+            return lds_ld(&sm.uready) >= c + 1 && lds_ld(&sm.cons) >= c - kHand + 1;
         });
         if (!ok) break;
         asm volatile("" ::: "memory");
-        const StageA& sa = sm.a[st];
+        StageA& sa = sm.a[st];
         // S at the chunk's start goes to the hand-off slot
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) sm.h[hs].S[h][kb][lane] = S16[kb];
+        for (int kb = 0; kb < 4; ++kb) sm.h[hs].S[kb][lane] = S16[kb];
         if (kDbg) {
-            float* dst = a.ws.dbgS + ((size_t)(chunk0 + c) * a.HV + hv) * kDK * kDV + col;
+            float* dst = a.ws.dbgS + ((size_t)(x.chunk0 + c) * a.HV + x.hv) * kDK * kDV + col;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) dst[(size_t)dk_of(t, i) * kDV] = S[t][i] + Sc[t][i];
+                for (int i = 0; i < 4; ++i) dst[(size_t)dk_of(t, i) * kDV] = S[t][i] + Sd[t][i];
             }
         }
-        // P = K S: row tile mt (tokens), k-block kb (dk)
-        f32x4 P[4];
+        // V_n = U + (-W) S16: row tile mt (tokens), k-block kb (dk)
+        f32x4 Vn[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) Vn[mt] = sa.U[mt][lane];
         {
-            half8 kf[4][4];
+            half8 wf[16];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const int r = 16 * mt + lm;
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-                    kf[mt][kb] = __builtin_bit_cast(half8, sa.K[16 * r + ((4 * kb + lg) ^ (r & 15))]);
-            }
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) P[mt] = zero4();
+            for (int f = 0; f < 16; ++f) wf[f] = sa.W[f][lane];
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) P[mt] = mfma16(kf[mt][kb], S16[kb], P[mt]);
+                for (int mt = 0; mt < 4; ++mt) Vn[mt] = mfma16(wf[mt * 4 + kb], S16[kb], Vn[mt]);
             }
         }
-        // R = beta o V - (beta e^c) o P: lane (lg, lm) of tile mt holds tokens
-        // 16 mt + 4 lg + i of column lm
-        f32x4 R[4], dec[4];
+        f32x4 dec[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const f32x4 be = *reinterpret_cast<const f32x4*>(&sa.beta[16 * mt + 4 * lg]);
-            const f32x4 bc = *reinterpret_cast<const f32x4*>(&sa.bec[16 * mt + 4 * lg]);
-            dec[mt] = *reinterpret_cast<const f32x4*>(&sa.dec[16 * mt + 4 * lg]);
-            // transposing read: source lane (a4 = lm / 4, b4 = lm % 4) names
-            // row 16 mt + 4 lg + a4, columns 8 b4 + 4 h .. + 3
-            const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(sa.V) +
-                                   (16 * mt + 4 * lg + (lm >> 2)) * kPairCols + 8 * (lm & 3) + 4 * h;
-            const s16x4 vt = lds_read_tr(vsrc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float vv = v16_to_f32<kRaw>((uint16_t)vt[i]);
-                R[mt][i] = be[i] * vv - bc[i] * P[mt][i];
-            }
-        }
-        const float gam = sa.gam;
-        half8 Rh[2];
-        Rh[0] = cat8(to_half4(R[0]), to_half4(R[1]));
-        Rh[1] = cat8(to_half4(R[2]), to_half4(R[3]));
-        // V_n = R + (T - I) R
-        f32x4 Vn[4];
-        {
-            half8 ti[kTri];
-#pragma unroll
-            for (int f = 0; f < kTri; ++f) ti[f] = sa.TI[f][lane];
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                Vn[mt] = mfma16(ti[tri_base(mt)], Rh[0], R[mt]);
-                if (mt >= 2) Vn[mt] = mfma16(ti[tri_base(mt) + 1], Rh[1], Vn[mt]);
-            }
-        }
-        half8 Vh[2];
-        Vh[0] = cat8(to_half4(Vn[0]), to_half4(Vn[1]));
-        Vh[1] = cat8(to_half4(Vn[2]), to_half4(Vn[3]));
-        sm.h[hs].V[h][0][lane] = Vh[0];
-        sm.h[hs].V[h][1][lane] = Vh[1];
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.ready[h], c + 1);
-        // d o V_n as an fp16 hi / lo pair
-        half8 hi[2], lo[2];
+        for (int mt = 0; mt < 4; ++mt)
+            dec[mt] = *reinterpret_cast<const f32x4*>(&sa.gates[kGDec + 16 * mt + 4 * lg]);
+        const float c63 = sa.gates[kGC63];
+        const float gam = __builtin_amdgcn_exp2f(c63 * kLog2e);
+        rem -= c63;
+        const float sig = __builtin_amdgcn_exp2f(rem * kLog2e);
+        // hand-off of V_n (fp16) for the output
+        sm.h[hs].V[0][lane] = cat8(to_half4(Vn[0]), to_half4(Vn[1]));
+        sm.h[hs].V[1][lane] = cat8(to_half4(Vn[2]), to_half4(Vn[3]));
+        // d o V_n as a bf16 hi / lo pair: B operand of token k-block kb
+        // (tiles 2kb, 2kb+1)
+        bf16x8 hi[2], lo[2], lou[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            f32x4 d0 = dec[2 * kb] * Vn[2 * kb], d1 = dec[2 * kb + 1] * Vn[2 * kb + 1];
-            const half4 h0 = to_half4(d0), h1 = to_half4(d1);
-            hi[kb] = cat8(h0, h1);
+            const f32x4 d0 = dec[2 * kb] * Vn[2 * kb], d1 = dec[2 * kb + 1] * Vn[2 * kb + 1];
+            u32x4 hw, lw;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                hw[p] = pack_bf16x2(d0[2 * p], d0[2 * p + 1]);
+                hw[2 + p] = pack_bf16x2(d1[2 * p], d1[2 * p + 1]);
+            }
             f32x4 r0, r1;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                r0[i] = d0[i] - (float)h0[i];
-                r1[i] = d1[i] - (float)h1[i];
+            for (int p = 0; p < 2; ++p) {
+                r0[2 * p] = (d0[2 * p] - __uint_as_float(hw[p] << 16)) * sig;
+                r0[2 * p + 1] = (d0[2 * p + 1] - __uint_as_float(hw[p] & 0xffff0000u)) * sig;
+                r1[2 * p] = (d1[2 * p] - __uint_as_float(hw[2 + p] << 16)) * sig;
+                r1[2 * p + 1] = (d1[2 * p + 1] - __uint_as_float(hw[2 + p] & 0xffff0000u)) * sig;
             }
-            lo[kb] = cat8(to_half4(r0), to_half4(r1));
-        }
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            S[t] = S[t] * gam;
-            Sc[t] = Sc[t] * gam;
+            for (int p = 0; p < 2; ++p) {
+                lw[p] = pack_bf16x2(r0[2 * p], r0[2 * p + 1]);
+                lw[2 + p] = pack_bf16x2(r1[2 * p], r1[2 * p + 1]);
+            }
+            hi[kb] = __builtin_bit_cast(bf16x8, hw);
+            lo[kb] = __builtin_bit_cast(bf16x8, lw);
+            if (kDbg) {
+                u32x4 uw;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    uw[p] = pack_bf16x2(d0[2 * p] - __uint_as_float(hw[p] << 16),
+                                        d0[2 * p + 1] - __uint_as_float(hw[p] & 0xffff0000u));
+                    uw[2 + p] = pack_bf16x2(d1[2 * p] - __uint_as_float(hw[2 + p] << 16),
+                                            d1[2 * p + 1] - __uint_as_float(hw[2 + p] & 0xffff0000u));
+                }
+                lou[kb] = __builtin_bit_cast(bf16x8, uw);
+            }
         }
-        // S' = e^{c63} S + K^T (d V_n): K^T fragment (tile t, k-block kb) from
-        // two transposing reads; source lane (a4 = lm / 4, b4 = lm % 4) names
-        // row tok0 + 4 lg + a4, dk 32 (t/2) + 8 b4 + 4 (t%2) .. + 3
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.ready, c + 1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) S[t] = S[t] * gam;
+        if (kDbg) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) Sd[t] = Sd[t] * gam;
+        }
+        // S' = e^{c63} S + K^T hi; Sc += K^T lo
         const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sa.K);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const int p = 4 * (t >> 1) + (lm & 3);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const int r0 = 32 * kb + 4 * lg + (lm >> 2), r1 = r0 + 16;
-                const s16x4 x0 = lds_read_tr(kbase + (16 * r0 + (p ^ (r0 & 15))) * 8 + 4 * (t & 1));
-                const s16x4 x1 = lds_read_tr(kbase + (16 * r1 + (p ^ (r1 & 15))) * 8 + 4 * (t & 1));
-                const half8 kt = cat8(s16x4_as_half4(x0), s16x4_as_half4(x1));
-                S[t] = mfma16(kt, hi[kb], S[t]);
-                Sc[t] = mfma16(kt, lo[kb], Sc[t]);
+                s16x4 x0, x1;
+                kt_reads(kbase, t, kb, lane, x0, x1);
+                const bf16x8 kt = tr_pair_bf16x8(x0, x1);
+                S[t] = mfma16_bf16(kt, hi[kb], S[t]);
+                Sc[t] = mfma16_bf16(kt, lo[kb], Sc[t]);
+                if (kDbg) Sd[t] = mfma16_bf16(kt, lou[kb], Sd[t]);
             }
         }
         lds_wait_all();
-        if (lane == 0) lds_st(&sm.freeA[h], c + 1);
+        if (lane == 0) lds_st(&sm.freeA, c + 1);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) S16[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
     }
@@ -1093,107 +1209,103 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, int 
 }
 
 template <int kRaw>
-__device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, int hv, int pr,
-                           int tok_base, int len, int nch, int lane) {
+__device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                           int lane) {
     const int lg = lane >> 4, lm = lane & 15;
-    for (int c = 0; c < nch; ++c) {
-        const int sb = c % kRingB, hs = c % kHand;
-        const bool ok = w.until([&] {
-            return min(lds_ld(&sm.fillB[0]), lds_ld(&sm.fillB[1])) >= c + 1 &&
-                   min(lds_ld(&sm.ready[0]), lds_ld(&sm.ready[1])) >= c + 1;
-        });
-        if (!ok) return;
+    // Q and M fragments and s e^c go straight to registers, one chunk ahead
+    half8 qf[16], mf[kTri], qn[16], mn[kTri];
+    float es[4], en[4];
+    auto load = [&](int c, half8 (&qd)[16], half8 (&md)[kTri], float (&ed)[4]) {
+        const int cc = min(c, x.nch - 1);
+        const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
+        const half8* qq = a.ws.Q + ((size_t)(x.chunk0 + cc) * a.HK + x.hk) * (16 * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < 16; ++f) qd[f] = qq[f * 64];
+        const half8* mm = a.ws.M + ch * (kTri * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < kTri; ++f) md[f] = mm[f * 64];
+        const float* gr = a.ws.gates + ch * (kGateBytes / 4) + kGSec + lm;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) ed[mt] = gr[16 * mt];
+    };
+    if (x.nch <= 0) return;
+    load(0, qf, mf, es);
+    for (int c = 0; c < x.nch; ++c) {
+        const int hs = c % kHand;
+        load(c + 1, qn, mn, en);
+        if (!w.until([&] { return lds_ld(&sm.ready) >= c + 1; })) return;
         asm volatile("" ::: "memory");
-        half8 hsf[2][4], hvf[2][2];
+        half8 hsf[4], hvf[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) hsf[h][kb] = sm.h[hs].S[h][kb][lane];
-            hvf[h][0] = sm.h[hs].V[h][0][lane];
-            hvf[h][1] = sm.h[hs].V[h][1][lane];
-        }
+        for (int kb = 0; kb < 4; ++kb) hsf[kb] = sm.h[hs].S[kb][lane];
+        hvf[0] = sm.h[hs].V[0][lane];
+        hvf[1] = sm.h[hs].V[1][lane];
         lds_wait_all();
         if (lane == 0) lds_st(&sm.cons, c + 1);
-        const StageB& stb = sm.b[sb];
-        half8 qf[4][4], mf[kTri];
-        float es[4];
+        // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T: lane (lg, lm) of tile mt
+        // holds columns 4 lg .. 4 lg + 3 of the slice for token 16 mt + lm
+        f32x4 ov[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) ov[mt] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) ov[mt] = mfma16(hsf[kb], qf[mt * 4 + kb], ov[mt]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            ov[mt] = ov[mt] * es[mt];
+            ov[mt] = mfma16(hvf[0], mf[tri_base(mt)], ov[mt]);
+            if (mt >= 2) ov[mt] = mfma16(hvf[1], mf[tri_base(mt) + 1], ov[mt]);
+        }
+        const int rows = min(kChunk, x.len - c * kChunk);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const int r = 16 * mt + lm;
+            uint2 pk;
+            uint32_t b[4];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-                qf[mt][kb] = __builtin_bit_cast(half8, stb.Q[16 * r + ((4 * kb + lg) ^ (r & 15))]);
-            es[mt] = stb.sec[r];
-        }
-#pragma unroll
-        for (int f = 0; f < kTri; ++f) mf[f] = stb.M[f][lane];
-        // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T per slice: lane (lg, lm)
-        // of tile mt holds columns 4 lg .. 4 lg + 3 of the slice for token
-        // 16 mt + lm
-        f32x4 ov[2][4];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) ov[h][mt] = zero4();
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) ov[h][mt] = mfma16(hsf[h][kb], qf[mt][kb], ov[h][mt]);
+            for (int e = 0; e < 4; ++e) {
+                b[e] = f32_to_bf16_bits(ov[mt][e]);
+                if constexpr (kRaw == 2) b[e] = f16_bits(__uint_as_float(b[e] << 16));
             }
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                ov[h][mt] = ov[h][mt] * es[mt];
-                ov[h][mt] = mfma16(hvf[h][0], mf[tri_base(mt)], ov[h][mt]);
-                if (mt >= 2) ov[h][mt] = mfma16(hvf[h][1], mf[tri_base(mt) + 1], ov[h][mt]);
-            }
-        }
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.freeB, c + 1);
-        const int rows = min(kChunk, len - c * kChunk);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const int r = 16 * mt + lm;
-            u32x4 pk;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const float x0 = ov[h][mt][2 * e], x1 = ov[h][mt][2 * e + 1];
-                    uint32_t b0 = f32_to_bf16_bits(x0), b1 = f32_to_bf16_bits(x1);
-                    if constexpr (kRaw == 2) {
-                        b0 = f16_bits(__uint_as_float(b0 << 16));
-                        b1 = f16_bits(__uint_as_float(b1 << 16));
-                    }
-                    pk[2 * h + e] = b0 | (b1 << 16);
-                }
-            }
+            pk.x = b[0] | (b[1] << 16);
+            pk.y = b[2] | (b[3] << 16);
             if (r < rows) {
-                u32x4* dst = reinterpret_cast<u32x4*>(
-                    a.o + ((size_t)(tok_base + c * kChunk + r) * a.HV + hv) * kDV + kPairCols * pr + 8 * lg);
+                uint2* dst = reinterpret_cast<uint2*>(
+                    a.o + ((size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv) * kDV +
+                    kSliceCols * x.sl + 4 * lg);
                 *dst = pk;
             }
         }
+#pragma unroll
+        for (int f = 0; f < 16; ++f) qf[f] = qn[f];
+#pragma unroll
+        for (int f = 0; f < kTri; ++f) mf[f] = mn[f];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) es[mt] = en[mt];
     }
 }
 
-// s0 and sf may be the same buffer: a chain reads its elements of the initial
-// state before its first chunk and writes the same elements after its last,
-// and no other wave touches either.
+// s0 and sf may be the same buffer: the chain reads its elements of the
+// initial state before its first chunk and writes the same elements after its
+// last, and no other wave touches either.
 template <int kRaw, bool kDbg>
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     __shared__ ScanSmem sm;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
 
-    // XCD-aware id: the four groups of one (sequence, head) share id % 8
-    // (one XCD, one L2), so their K, Q, T - I and M come from one L2
+    // XCD-aware id: the eight groups of one (sequence, head) share id % 8
+    // (one XCD, one L2), so their K, -W, Q and M come from one L2
     const int id = blockIdx.x;
     const int xcd = id & 7, qd = id >> 3;
-    const int pr = qd % kPairsPerHead;
-    const int pidx = (qd / kPairsPerHead) * 8 + xcd;
+    ScanCtx x;
+    x.sl = qd % kSlicesPerHead;
+    const int pidx = (qd / kSlicesPerHead) * 8 + xcd;
     if (pidx >= a.N * a.HV) return;
-    int seq = pidx / a.HV;
-    const int hv = pidx - seq * a.HV;
+    x.seq = pidx / a.HV;
+    x.hv = pidx - x.seq * a.HV;
     // Packed sequences of different lengths: groups start in id order as CUs
     // free up, so the low ids go to the longest sequences (longest first).
     if (a.cu && a.N <= kScanThreads) {
@@ -1204,44 +1316,37 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
                 const int lu = seq_count(a.cu, a.T, a.total, u);
                 rank += (lu > my || (lu == my && u < tid)) ? 1 : 0;
             }
-            if (rank == seq) sm.seqsel = tid;
+            if (rank == x.seq) sm.seqsel = tid;
         }
         __syncthreads();
-        seq = sm.seqsel;
+        x.seq = sm.seqsel;
     }
-    const int hk = hv / (a.HV / a.HK);
-    const int len = seq_count(a.cu, a.T, a.total, seq);
-    const int tok_base = seq_lo(a.cu, a.T, a.total, seq);
-    const int chunk0 = __builtin_amdgcn_readfirstlane(
-        chunks_before<kScanThreads>(a.cu, a.T, a.total, seq, sm.red));
-    const int nch = seq_chunks_bounded(a.cu, a.T, a.total, seq, chunk0, a.nch_bound);
-    if (tid < 2) {
-        lds_st(&sm.fillA[tid], 0);
-        lds_st(&sm.fillB[tid], 0);
-        lds_st(&sm.freeA[tid], 0);
-        lds_st(&sm.ready[tid], 0);
-    }
+    x.hk = x.hv / (a.HV / a.HK);
+    x.len = seq_count(a.cu, a.T, a.total, x.seq);
+    x.tok_base = seq_lo(a.cu, a.T, a.total, x.seq);
+    x.chunk0 = __builtin_amdgcn_readfirstlane(
+        chunks_before<kScanThreads>(a.cu, a.T, a.total, x.seq, sm.red));
+    x.nch = seq_chunks_bounded(a.cu, a.T, a.total, x.seq, x.chunk0, a.nch_bound);
     if (tid == 0) {
-        lds_st(&sm.freeB, 0);
+        lds_st(&sm.fillA, 0);
+        lds_st(&sm.uready, 0);
+        lds_st(&sm.freeA, 0);
+        lds_st(&sm.ready, 0);
         lds_st(&sm.cons, 0);
         lds_st(&sm.abort, 0);
     }
     __syncthreads();
     const Waiter w{&sm.abort, a.ws.status, a.spin};
-    const float scale = 1.0f / sqrtf((float)kDK);
     switch (wave) {
-        case 0: run_chain<kRaw, kDbg>(sm, a, w, 0, seq, hv, pr, chunk0, nch, lane); break;
-        case 1: run_chain<kRaw, kDbg>(sm, a, w, 1, seq, hv, pr, chunk0, nch, lane); break;
-        case 2: run_output<kRaw>(sm, a, w, hv, pr, tok_base, len, nch, lane); break;
-        case 3: run_row_loader<false, kRaw>(sm, a, w, hk, hv, tok_base, len, nch, scale, lane); break;
-        case 6: run_aux_loader(sm, a, w, hv, pr, tok_base, len, chunk0, nch, lane); break;
-        case 7: run_row_loader<true, kRaw>(sm, a, w, hk, hv, tok_base, len, nch, scale, lane); break;
-        default: break;   // waves 4, 5: each chain keeps its SIMD to itself
+        case 0: run_chain<kDbg>(sm, a, w, x, lane); break;
+        case 1: run_producer<kRaw>(sm, a, w, x, lane); break;
+        case 2: run_output<kRaw>(sm, a, w, x, lane); break;
+        default: run_loader(sm, a, w, x, lane); break;
     }
 }
 
 // raw: 0 for prepared inputs, 1 / 2 for raw bf16 / fp16 q, k (normalised in
-// the kernels; then v and o have that dtype too).
+// the prep; then v and o have that dtype too).
 hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
@@ -1253,7 +1358,12 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     char* base = static_cast<char*>(workspace);
     Workspace ws{};
     ws.TI = reinterpret_cast<half8*>(base + L.ti);
+    ws.TIlo = reinterpret_cast<half8*>(base + L.tilo);
     ws.M = reinterpret_cast<half8*>(base + L.m);
+    ws.W = reinterpret_cast<half8*>(base + L.w);
+    ws.gates = reinterpret_cast<float*>(base + L.gates);
+    ws.Q = reinterpret_cast<half8*>(base + L.q);
+    ws.Kn = reinterpret_cast<uint16_t*>(base + L.kn);
     ws.status = reinterpret_cast<unsigned*>(base);
     if (dump_debug) {
         ws.dbgT = reinterpret_cast<float*>(base + L.dbgT);
@@ -1288,6 +1398,7 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     sa.s0 = s0;
     sa.sf = sf;
     sa.cu = cu;
+    sa.krows = raw ? ws.Kn : in.k;
     sa.N = N;
     sa.T = T;
     sa.total = total_tokens;
@@ -1300,7 +1411,7 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     auto scan = raw == 1 ? gdn_scan_kernel<1, false>
                 : raw == 2 ? gdn_scan_kernel<2, false>
                 : dump_debug ? gdn_scan_kernel<0, true> : gdn_scan_kernel<0, false>;
-    hipLaunchKernelGGL(scan, dim3((unsigned)(grp * 8 * kPairsPerHead)), dim3(kScanThreads), 0,
+    hipLaunchKernelGGL(scan, dim3((unsigned)(grp * 8 * kSlicesPerHead)), dim3(kScanThreads), 0,
                        stream, sa);
     hipError_t err = hipGetLastError();
     if (ev) (void)hipEventRecord(ev[2], stream);
