@@ -34,6 +34,10 @@ HIPCC_FLAGS = [
     "-shared",
     # packed fp32 VALU ops stay off (hipcc flag; the host pass warns, harmlessly)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the scan scales and converts its state
+    # accumulators with VALU every chunk, which AGPR accumulators would turn
+    # into accvgpr read / write round trips
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -59,7 +59,6 @@ namespace gdn {
 namespace {
 
 constexpr int kPrepThreads = 256;
-constexpr int kScanThreads = 256;
 constexpr int kSliceCols = 16;                     // value columns per scan work-group
 constexpr int kSlicesPerHead = kDV / kSliceCols;   // 8
 constexpr int kTri = 6;                            // nonzero (row tile, k-block) fragments of a lower-triangular 64x64
@@ -774,8 +773,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (4 waves, one per SIMD) per (16 value columns,
-// v-head, sequence).
+// scan kernel: one work-group (6 waves) per (16 value columns, v-head,
+// sequence).
 //
 // State layout of the chain: accumulator tile t (0..7), lane (g, n), element
 // i holds S[dk][16 sl + n] with dk = 32 (t/2) + 8 g + 4 (t%2) + i, so the
@@ -787,23 +786,39 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
 //             S' = e^{c63} S + K^T hi (16 bf16 MFMA), Sc += K^T (sigma lo)
 //             (16 bf16 MFMA, off the serial path: sigma = e^{sum of the
 //             later chunks' c63} pre-applies the decay the lo part would
-//             see, so Sc needs no per-chunk scaling).
+//             see, so Sc needs no per-chunk scaling).  Wave 4, on the same
+//             SIMD, exits at once.
 //   producer  wave 1: U = beta V + (T - I)(beta V) with the product as
-//             hi/hi + hi/lo + lo/hi fp16 MFMAs (18), into ring A.
-//   output    wave 2: O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T, with Q, M and
-//             s e^c loaded to registers one chunk ahead.
-//   loader    wave 3: K rows, -W, V and the gates record into ring A as
-//             direct-to-LDS loads.
+//             hi/hi + hi/lo + lo/hi fp16 MFMAs (18), into ring P.
+//   output    waves 2 and 3, chunks of even and odd index:
+//             O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T, with Q, M and s e^c
+//             loaded to registers as soon as the wave's previous chunk has
+//             read them, two chain steps before they are needed.
+//   loader    wave 5 (on the producer's SIMD): direct-to-LDS loads of K rows
+//             and -W into ring C (3 stages, 32 KB each) and of V and the
+//             gates record into ring P (5 stages, 7 KB each, filled two chunks
+//             ahead of ring C), plus L2 warm-up loads of the K rows and -W
+//             two chunks ahead of their ring-C loads.
 // ---------------------------------------------------------------------------
-constexpr int kRingA = 3;     // chain operand stages
-constexpr int kHand = 2;      // chain -> output hand-off slots
+constexpr int kRingC = 3;     // chain operand stages (K rows, -W)
+constexpr int kRingP = 4;     // producer stages (V, gates, U)
+constexpr int kLeadP = 1;     // ring P is filled this many chunks ahead of ring C
+constexpr int kLoSlots = 2;   // chain -> lo-helper hand-off slots
+constexpr int kHand = 4;      // chain -> output hand-off slots
+constexpr int kScanWaves = 6;
+constexpr int kScanThreads = 64 * kScanWaves;
+static_assert(kRingP >= kRingC + kLeadP, "ring P must hold the chunks ring C and the lead span");
+static_assert(kHand % 2 == 0, "a hand-off slot is reused by a chunk of the same parity");
 
-struct StageA {
+struct StageC {
     u32x4 K[kChunk * 16];   // bf16 K rows, row_slot layout
     half8 W[16][64];        // -W fragments (mt * 4 + kb)
-    f32x4 U[4][64];         // U, D layout per row tile (producer)
+};
+
+struct StageP {
     u32x4 V[kChunk * 2];    // V rows of the slice's 16 columns, 2 pieces per row
     float gates[256];       // gates record
+    f32x4 U[4][64];         // U, D layout per row tile (producer)
 };
 
 struct Hand {
@@ -811,17 +826,29 @@ struct Hand {
     half8 V[2][64];         // V_n, fp16 B fragments
 };
 
+struct LoHand {
+    f32x4 d[4][64];         // d o V_n (fp32, D layout per row tile)
+    float sig;              // sigma of the chunk
+    float pad_[63];
+};
+
 struct ScanSmem {
-    StageA a[kRingA];
+    StageC c[kRingC];
+    StageP p[kRingP];
     Hand h[kHand];
-    int fillA;       // chunks whose ring-A loads have landed (loader)
-    int uready;      // chunks whose U is in ring A (producer)
-    int freeA;       // chunks whose ring-A stage the chain has finished reading
+    LoHand lo[kLoSlots];   // after the last chunk: the helper's Sc (8 KB)
+    int fillC;       // chunks whose ring-C loads have landed (loader)
+    int fillP;       // chunks whose ring-P loads have landed (loader)
+    int uready;      // chunks whose U is in ring P (producer)
+    int freeC;       // chunks whose ring-C and ring-P stages the chain has finished reading
     int ready;       // chunks whose hand-off slot the chain has written
-    int cons;        // chunks whose hand-off slot the output has read
+    int cons[2];     // per output wave: chunks of its parity whose hand-off slot it has read
+    int dvready;     // chunks whose d o V_n the chain has handed to the helper
+    int lodone;      // chunks whose lo part the helper has accumulated
+    int scdone;      // the helper's Sc is in the lo slots
     int abort;       // a bounded wait ran out: every wave stops
     int seqsel;
-    int red[kScanThreads / 64];
+    int red[kScanWaves];
 };
 
 __device__ __forceinline__ int lds_ld(const int* p) {
@@ -888,27 +915,39 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
-// Loader: 35 direct-to-LDS loads per chunk (16 for K rows, 16 for -W, 2 for
-// V, 1 for the gates).  A chunk's loads go out as soon as its stage is free;
-// its counter is set as soon as they have landed.  The next chunk's loads are
-// issued first when its stage is already free, so two chunks can be in
-// flight.
-constexpr int kLoadsPerChunk = 35;
 // s_waitcnt immediates: vmcnt(n) with expcnt and lgkmcnt left at their
 // maxima; vmcnt's 6 bits are split over bits 3:0 and 15:14
 constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
-constexpr unsigned kVmcntOneChunk = vmcnt_imm(kLoadsPerChunk);
-constexpr unsigned kVmcntBeforeNext = vmcnt_imm(63 - kLoadsPerChunk);
 static_assert(vmcnt_imm(16) == 0x4F70 && vmcnt_imm(0) == 0x0F70, "s_waitcnt encoding");
+
+// Loader step c issues one group of direct-to-LDS loads: ring P for chunk
+// c + kLeadP (V: 2, gates: 1) and ring C for chunk c (K rows: 16, -W: 16).
+// Past the sequence's end the ring-P index is clamped, so every group holds
+// the same number of loads.
+constexpr int kGroupLoads = 3 + 32;
+constexpr unsigned kVmcntGroup = vmcnt_imm(kGroupLoads);
+constexpr unsigned kVmcntRoom = vmcnt_imm(63 - kGroupLoads);   // at most 63 in flight
 
 __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                            int lane) {
-    auto stage_free = [&](int c) { return lds_ld(&sm.freeA) >= c - kRingA + 1; };
-    auto issue = [&](int c) {
-        asm volatile("" ::: "memory");
-        StageA& st = sm.a[c % kRingA];
-        const int t0 = x.tok_base + c * kChunk, rows = min(kChunk, x.len - c * kChunk);
-        const size_t ch = (size_t)(x.chunk0 + c) * a.HV + x.hv;
+    auto rows_of = [&](int c) { return min(kChunk, x.len - c * kChunk); };
+    auto ch_of = [&](int c) { return (size_t)(x.chunk0 + c) * a.HV + x.hv; };
+    auto issue_p = [&](int cp) {
+        const int c = min(cp, x.nch - 1);
+        StageP& st = sm.p[cp % kRingP];
+        const int t0 = x.tok_base + c * kChunk, rows = rows_of(c);
+        // V: slot 64 i + lane -> row (64 i + lane) / 2, piece lane % 2
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int s = 64 * i + lane, r = min(s >> 1, rows - 1);
+            lds_dma16(a.in.v + ((size_t)(t0 + r) * a.HV + x.hv) * kDV + kSliceCols * x.sl + 8 * (s & 1),
+                      &st.V[64 * i]);
+        }
+        lds_dma16(a.ws.gates + ch_of(c) * (kGateBytes / 4) + 4 * lane, &st.gates[0]);
+    };
+    auto issue_c = [&](int c) {
+        StageC& st = sm.c[c % kRingC];
+        const int t0 = x.tok_base + c * kChunk, rows = rows_of(c);
         // K rows: slot s = 64 i + lane -> row s / 16, stored piece s % 16,
         // which is source piece (s % 16) ^ (row % 16)
 #pragma unroll
@@ -917,43 +956,45 @@ __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
             const int rr = min(r, rows - 1);
             lds_dma16(a.krows + ((size_t)(t0 + rr) * a.HK + x.hk) * kDK + 8 * p, &st.K[64 * i]);
         }
-        const half8* wsrc = a.ws.W + ch * (16 * 64) + lane;
+        const half8* wsrc = a.ws.W + ch_of(c) * (16 * 64) + lane;
 #pragma unroll
         for (int f = 0; f < 16; ++f) lds_dma16(wsrc + f * 64, &st.W[f][0]);
-        // V: slot 64 i + lane -> row (64 i + lane) / 2, piece lane % 2
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int s = 64 * i + lane, r = min(s >> 1, rows - 1);
-            lds_dma16(a.in.v + ((size_t)(t0 + r) * a.HV + x.hv) * kDV + kSliceCols * x.sl + 8 * (s & 1),
-                      &st.V[64 * i]);
-        }
-        lds_dma16(a.ws.gates + ch * (kGateBytes / 4) + 4 * lane, &st.gates[0]);
     };
     if (x.nch <= 0) return;
-    issue(0);   // stage 0 starts free
+    // prologue: ring P for chunks 0 .. kLeadP - 1
+    for (int c = 0; c < kLeadP; ++c) issue_p(c);
+    vm_wait_all();
+    if (lane == 0) lds_st(&sm.fillP, kLeadP);
     for (int c = 0; c < x.nch; ++c) {
-        const bool more = c + 1 < x.nch;
-        const bool ahead = more && stage_free(c + 1);
-        if (ahead) {
-            // at most 63 loads outstanding (the counter's range): let chunk
-            // c drain to 63 - 35 before chunk c + 1 goes out
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_waitcnt(kVmcntBeforeNext);
-            issue(c + 1);
-            // chunk c's loads have landed, chunk c + 1's may be in flight
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_waitcnt(kVmcntOneChunk);
-            asm volatile("" ::: "memory");
-        } else {
-            vm_wait_all();
+        // ring-C stage c % kRingC held chunk c - kRingC (read by the chain
+        // and the lo helper); ring-P stage (c + kLeadP) % kRingP held chunk
+        // c + kLeadP - kRingP <= c - kRingC
+        if (!w.until([&] {
+                return min(lds_ld(&sm.freeC), lds_ld(&sm.lodone)) >= c - kRingC + 1;
+            })) {
+            vm_wait_all();   // no load may land in LDS after the group ends
+            return;
         }
-        if (lane == 0) lds_st(&sm.fillA, c + 1);
-        if (more && !ahead) {
-            if (!w.until([&] { return stage_free(c + 1); })) return;   // nothing in flight
-            issue(c + 1);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(kVmcntRoom);
+        issue_p(c + kLeadP);
+        issue_c(c);
+        if (c > 0) {
+            // group c - 1 has landed (group c may be in flight)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(kVmcntGroup);
+            asm volatile("" ::: "memory");
+            if (lane == 0) {
+                lds_st(&sm.fillC, c);
+                lds_st(&sm.fillP, c + kLeadP);
+            }
         }
     }
     vm_wait_all();
+    if (lane == 0) {
+        lds_st(&sm.fillC, x.nch);
+        lds_st(&sm.fillP, x.nch + kLeadP);
+    }
 }
 
 template <int kRaw>
@@ -963,7 +1004,7 @@ __device__ inline float v16_to_f32(uint32_t bits) {
     return __uint_as_float(bits << 16);
 }
 
-// Producer: U = beta V + (T - I)(beta V) per chunk into ring A.  With X =
+// Producer: U = beta V + (T - I)(beta V) per chunk into ring P.  With X =
 // beta V (fp32, D layout), the product is (T-I)_hi X_hi + (T-I)_hi X_lo +
 // (T-I)_lo X_hi on fp16 MFMA, accumulated onto X.
 template <int kRaw>
@@ -986,9 +1027,9 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
     load_t(0, th, tl);
     for (int c = 0; c < x.nch; ++c) {
         load_t(c + 1, nh, nl);
-        if (!w.until([&] { return lds_ld(&sm.fillA) >= c + 1; })) return;
+        if (!w.until([&] { return lds_ld(&sm.fillP) >= c + 1; })) return;
         asm volatile("" ::: "memory");
-        StageA& st = sm.a[c % kRingA];
+        StageP& st = sm.p[c % kRingP];
         // X = beta V: lane (g, n) of tile mt holds tokens 16 mt + 4 g + i of
         // column n (transposing read: source lane (a4 = lm / 4, b4 = lm % 4)
         // names row 16 mt + 4 lg + a4, columns 4 b4 .. + 3)
@@ -1040,8 +1081,20 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
     }
 }
 
+// Two floats as a packed bf16 pair (round to nearest even), one
+// v_cvt_pk_bf16_f32
 __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Hand-off slot c % kHand is free once the chunk that used it before,
+// c - kHand (same parity), has been read by its output wave.
+__device__ inline bool slot_free(const ScanSmem& sm, int c) {
+    const int prev = c - kHand;
+    return prev < 0 || lds_ld(&sm.cons[prev & 1]) >= (prev >> 1) + 1;
 }
 
 template <bool kDbg>
@@ -1074,15 +1127,13 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
     // remaining log-decay after each chunk: rem = sum of c63 over the later
     // chunks of this sequence; starts as the total
     float rem = 0.f;
-    {
-        for (int j0 = 0; j0 < x.nch; j0 += 64) {
-            const int j = j0 + lane;
-            float v = 0.f;
-            if (j < x.nch) v = a.ws.gates[((size_t)(x.chunk0 + j) * a.HV + x.hv) * (kGateBytes / 4) + kGC63];
+    for (int j0 = 0; j0 < x.nch; j0 += 64) {
+        const int j = j0 + lane;
+        float v = 0.f;
+        if (j < x.nch) v = a.ws.gates[((size_t)(x.chunk0 + j) * a.HV + x.hv) * (kGateBytes / 4) + kGC63];
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-            rem += v;
-        }
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        rem += v;
     }
 
     half8 S16[4];
@@ -1091,16 +1142,35 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
 
     bool ok = true;
     for (int c = 0; c < x.nch; ++c) {
-        const int st = c % kRingA, hs = c % kHand;
+        const int hs = c % kHand;
         ok = w.until([&] {
-            return lds_ld(&sm.uready) >= c + 1 && lds_ld(&sm.cons) >= c - kHand + 1;
+            return lds_ld(&sm.fillC) >= c + 1 && lds_ld(&sm.uready) >= c + 1 && slot_free(sm, c) &&
+                   (kDbg || lds_ld(&sm.lodone) >= c - kLoSlots + 1);
         });
         if (!ok) break;
         asm volatile("" ::: "memory");
-        StageA& sa = sm.a[st];
-        // S at the chunk's start goes to the hand-off slot
+        StageC& sc = sm.c[c % kRingC];
+        StageP& sp = sm.p[c % kRingP];
+        // The step is laid out in issue order: every LDS read of a phase goes
+        // out before the phase's products, and the K^T reads of the state
+        // update go out behind the V_n products, so no product waits on a
+        // read issued just before it.
+        // (1) reads for V_n: U (accumulator init), -W, the gates
+        f32x4 Vn[4], dec[4];
+        half8 wf[16];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) sm.h[hs].S[kb][lane] = S16[kb];
+        for (int mt = 0; mt < 4; ++mt) Vn[mt] = sp.U[mt][lane];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) wf[mt * 4 + kb] = sc.W[mt * 4 + kb][lane];
+        }
+        const float c63 = sp.gates[kGC63];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            dec[mt] = *reinterpret_cast<const f32x4*>(&sp.gates[kGDec + 16 * mt + 4 * lg]);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of the products
         if (kDbg) {
             float* dst = a.ws.dbgS + ((size_t)(x.chunk0 + c) * a.HV + x.hv) * kDK * kDV + col;
 #pragma unroll
@@ -1109,98 +1179,137 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
                 for (int i = 0; i < 4; ++i) dst[(size_t)dk_of(t, i) * kDV] = S[t][i] + Sd[t][i];
             }
         }
-        // V_n = U + (-W) S16: row tile mt (tokens), k-block kb (dk)
-        f32x4 Vn[4];
+        // (2) V_n = U + (-W) S16: row tile mt (tokens), k-block kb (dk)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) Vn[mt] = sa.U[mt][lane];
-        {
-            half8 wf[16];
+        for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-            for (int f = 0; f < 16; ++f) wf[f] = sa.W[f][lane];
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) Vn[mt] = mfma16(wf[mt * 4 + kb], S16[kb], Vn[mt]);
-            }
+            for (int mt = 0; mt < 4; ++mt) Vn[mt] = mfma16(wf[mt * 4 + kb], S16[kb], Vn[mt]);
         }
-        f32x4 dec[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            dec[mt] = *reinterpret_cast<const f32x4*>(&sa.gates[kGDec + 16 * mt + 4 * lg]);
-        const float c63 = sa.gates[kGC63];
-        const float gam = __builtin_amdgcn_exp2f(c63 * kLog2e);
-        rem -= c63;
-        const float sig = __builtin_amdgcn_exp2f(rem * kLog2e);
-        // hand-off of V_n (fp16) for the output
-        sm.h[hs].V[0][lane] = cat8(to_half4(Vn[0]), to_half4(Vn[1]));
-        sm.h[hs].V[1][lane] = cat8(to_half4(Vn[2]), to_half4(Vn[3]));
-        // d o V_n as a bf16 hi / lo pair: B operand of token k-block kb
-        // (tiles 2kb, 2kb+1)
-        bf16x8 hi[2], lo[2], lou[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const f32x4 d0 = dec[2 * kb] * Vn[2 * kb], d1 = dec[2 * kb + 1] * Vn[2 * kb + 1];
-            u32x4 hw, lw;
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                hw[p] = pack_bf16x2(d0[2 * p], d0[2 * p + 1]);
-                hw[2 + p] = pack_bf16x2(d1[2 * p], d1[2 * p + 1]);
-            }
-            f32x4 r0, r1;
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                r0[2 * p] = (d0[2 * p] - __uint_as_float(hw[p] << 16)) * sig;
-                r0[2 * p + 1] = (d0[2 * p + 1] - __uint_as_float(hw[p] & 0xffff0000u)) * sig;
-                r1[2 * p] = (d1[2 * p] - __uint_as_float(hw[2 + p] << 16)) * sig;
-                r1[2 * p + 1] = (d1[2 * p + 1] - __uint_as_float(hw[2 + p] & 0xffff0000u)) * sig;
-            }
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                lw[p] = pack_bf16x2(r0[2 * p], r0[2 * p + 1]);
-                lw[2 + p] = pack_bf16x2(r1[2 * p], r1[2 * p + 1]);
-            }
-            hi[kb] = __builtin_bit_cast(bf16x8, hw);
-            lo[kb] = __builtin_bit_cast(bf16x8, lw);
-            if (kDbg) {
-                u32x4 uw;
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    uw[p] = pack_bf16x2(d0[2 * p] - __uint_as_float(hw[p] << 16),
-                                        d0[2 * p + 1] - __uint_as_float(hw[p] & 0xffff0000u));
-                    uw[2 + p] = pack_bf16x2(d1[2 * p] - __uint_as_float(hw[2 + p] << 16),
-                                            d1[2 * p + 1] - __uint_as_float(hw[2 + p] & 0xffff0000u));
-                }
-                lou[kb] = __builtin_bit_cast(bf16x8, uw);
-            }
-        }
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.ready, c + 1);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) S[t] = S[t] * gam;
-        if (kDbg) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) Sd[t] = Sd[t] * gam;
-        }
-        // S' = e^{c63} S + K^T hi; Sc += K^T lo
-        const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sa.K);
+        // (3) K^T operands of the state update (32 transposing reads)
+        const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sc.K);
+        bf16x8 kt[8][2];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 s16x4 x0, x1;
                 kt_reads(kbase, t, kb, lane, x0, x1);
-                const bf16x8 kt = tr_pair_bf16x8(x0, x1);
-                S[t] = mfma16_bf16(kt, hi[kb], S[t]);
-                Sc[t] = mfma16_bf16(kt, lo[kb], Sc[t]);
-                if (kDbg) Sd[t] = mfma16_bf16(kt, lou[kb], Sd[t]);
+                kt[t][kb] = tr_pair_bf16x8(x0, x1);
             }
         }
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.freeA, c + 1);
+        // (4) decay of the state while the V_n products run; S at the
+        // chunk's start goes to the hand-off slot
+        const float gam = __builtin_amdgcn_exp2f(c63 * kLog2e);
+        rem -= c63;
+        const float sig = __builtin_amdgcn_exp2f(rem * kLog2e);
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) S16[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
+        for (int kb = 0; kb < 4; ++kb) sm.h[hs].S[kb][lane] = S16[kb];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) S[t] = S[t] * gam;
+        if (kDbg) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) Sd[t] = Sd[t] * gam;
+        }
+        // A wave issues in order: each product is followed by independent
+        // VALU work and reads, so they run while the product is in the
+        // matrix pipe instead of after all products.
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS read
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // (5) d o V_n, hi part (bf16): B operand of token k-block kb (tiles
+        // 2kb, 2kb+1)
+        f32x4 dv[4];
+        u32x4 hw[2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            dv[mt] = dec[mt] * Vn[mt];
+            // rounded here, as the helper sees it: no later use may fuse
+            // the product into an FMA
+            asm volatile("" : "+v"(dv[mt]));
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int p = 0; p < 2; ++p)
+                    hw[kb][2 * h + p] = pack_bf16x2(dv[2 * kb + h][2 * p], dv[2 * kb + h][2 * p + 1]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (6) d o V_n (and sigma) to the lo helper on this SIMD, which adds
+        // K^T (sigma lo) to its Sc off the serial path (the debug build keeps
+        // that work here, with Sd beside it)
+        if (!kDbg) {
+            LoHand& lh = sm.lo[c % kLoSlots];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) lh.d[mt][lane] = dv[mt];
+            if (lane == 0) lh.sig = sig;
+            lds_wait_all();
+            if (lane == 0) lds_st(&sm.dvready, c + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (7) S' = e^{c63} S + K^T hi.  Issue order is fixed piece by piece
+        // (the wave issues in order): the lo-part VALU (debug build) and the
+        // S16 and V_n conversions are spread between the products.
+        u32x4 lw[2], uw[2];
+        auto lo_pair = [&](int kb, int q) {   // q = 2 h + p: one packed pair
+            const int h = q >> 1, p = q & 1;
+            const f32x4& d = dv[2 * kb + h];
+            const uint32_t hp = hw[kb][q];
+            const float r0 = d[2 * p] - __uint_as_float(hp << 16);
+            const float r1 = d[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
+            lw[kb][q] = pack_bf16x2(r0 * sig, r1 * sig);
+            uw[kb][q] = pack_bf16x2(r0, r1);
+        };
+        half8 vh[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf16x8 hi = __builtin_bit_cast(bf16x8, hw[kb]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                S[t] = mfma16_bf16(kt[t][kb], hi, S[t]);
+                if (kDbg && (t & 1)) lo_pair(kb, t >> 1);
+                if (kb == 0 && t < 2) vh[t] = cat8(to_half4(Vn[2 * t]), to_half4(Vn[2 * t + 1]));
+                if (kb == 1 && (t & 1))
+                    S16[t >> 1] = cat8(to_half4(S[t - 1]), to_half4(S[t]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (kDbg) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    Sc[t] = mfma16_bf16(kt[t][kb], __builtin_bit_cast(bf16x8, lw[kb]), Sc[t]);
+                    Sd[t] = mfma16_bf16(kt[t][kb], __builtin_bit_cast(bf16x8, uw[kb]), Sd[t]);
+                }
+            }
+        }
+        // (7) hand-off of V_n (fp16) for the output
+        sm.h[hs].V[0][lane] = vh[0];
+        sm.h[hs].V[1][lane] = vh[1];
+        __builtin_amdgcn_sched_barrier(0);
+        lds_wait_all();
+        if (lane == 0) {
+            lds_st(&sm.ready, c + 1);
+            lds_st(&sm.freeC, c + 1);
+        }
     }
     if (!ok) return;
+    if (!kDbg && x.nch > 0) {
+        // the helper's Sc, left in the lo slots after its last chunk
+        if (!w.until([&] { return lds_ld(&sm.scdone) != 0; })) return;
+        asm volatile("" ::: "memory");
+        const f32x4* src = &sm.lo[0].d[0][0];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) Sc[t] = src[t * 64 + lane];
+    }
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
 #pragma unroll
@@ -1208,31 +1317,96 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
     }
 }
 
+// Lo helper (the chain's SIMD): Sc += K^T (sigma lo) per chunk, with d o V_n
+// from the chain split again into its bf16 hi part and the residual lo =
+// bf16(sigma (d o V_n - hi)), the same values the chain's hi part leaves out.
+// A single wave issues about half of its SIMD's MFMA rate, so these products
+// run beside the chain's instead of after them.  After the last chunk Sc goes
+// to the lo slots for the chain.
+__device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                              int lane) {
+    f32x4 Sc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) Sc[t] = zero4();
+    if (x.nch <= 0) return;
+    for (int c = 0; c < x.nch; ++c) {
+        if (!w.until([&] { return lds_ld(&sm.dvready) >= c + 1; })) return;
+        asm volatile("" ::: "memory");
+        const LoHand& lh = sm.lo[c % kLoSlots];
+        f32x4 d[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) d[mt] = lh.d[mt][lane];
+        const float sig = lh.sig;
+        const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sm.c[c % kRingC].K);
+        bf16x8 kt[8][2];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                s16x4 x0, x1;
+                kt_reads(kbase, t, kb, lane, x0, x1);
+                kt[t][kb] = tr_pair_bf16x8(x0, x1);
+            }
+        }
+        bf16x8 lo[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            u32x4 lw;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const f32x4& dd = d[2 * kb + h];
+                    const uint32_t hp = pack_bf16x2(dd[2 * p], dd[2 * p + 1]);
+                    const float r0 = dd[2 * p] - __uint_as_float(hp << 16);
+                    const float r1 = dd[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
+                    lw[2 * h + p] = pack_bf16x2(r0 * sig, r1 * sig);
+                }
+            }
+            lo[kb] = __builtin_bit_cast(bf16x8, lw);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) Sc[t] = mfma16_bf16(kt[t][kb], lo[kb], Sc[t]);
+        }
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.lodone, c + 1);
+    }
+    // every chunk's slot has been read: Sc goes to the lo slots
+    f32x4* dst = &sm.lo[0].d[0][0];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) dst[t * 64 + lane] = Sc[t];
+    lds_wait_all();
+    if (lane == 0) lds_st(&sm.scdone, 1);
+}
+
+// Output wave j (0 or 1): chunks j, j + 2, ...
 template <int kRaw>
 __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
-                           int lane) {
+                           int j, int lane) {
     const int lg = lane >> 4, lm = lane & 15;
-    // Q and M fragments and s e^c go straight to registers, one chunk ahead
-    half8 qf[16], mf[kTri], qn[16], mn[kTri];
-    float es[4], en[4];
-    auto load = [&](int c, half8 (&qd)[16], half8 (&md)[kTri], float (&ed)[4]) {
+    // Q and M fragments and s e^c go straight to registers; the next chunk's
+    // loads are issued as soon as the current chunk's products have read them
+    half8 qf[16], mf[kTri];
+    float es[4];
+    auto load = [&](int c) {
         const int cc = min(c, x.nch - 1);
         const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
         const half8* qq = a.ws.Q + ((size_t)(x.chunk0 + cc) * a.HK + x.hk) * (16 * 64) + lane;
 #pragma unroll
-        for (int f = 0; f < 16; ++f) qd[f] = qq[f * 64];
+        for (int f = 0; f < 16; ++f) qf[f] = qq[f * 64];
         const half8* mm = a.ws.M + ch * (kTri * 64) + lane;
 #pragma unroll
-        for (int f = 0; f < kTri; ++f) md[f] = mm[f * 64];
+        for (int f = 0; f < kTri; ++f) mf[f] = mm[f * 64];
         const float* gr = a.ws.gates + ch * (kGateBytes / 4) + kGSec + lm;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) ed[mt] = gr[16 * mt];
+        for (int mt = 0; mt < 4; ++mt) es[mt] = gr[16 * mt];
     };
-    if (x.nch <= 0) return;
-    load(0, qf, mf, es);
-    for (int c = 0; c < x.nch; ++c) {
+    if (j >= x.nch) return;
+    load(j);
+    for (int c = j; c < x.nch; c += 2) {
         const int hs = c % kHand;
-        load(c + 1, qn, mn, en);
         if (!w.until([&] { return lds_ld(&sm.ready) >= c + 1; })) return;
         asm volatile("" ::: "memory");
         half8 hsf[4], hvf[2];
@@ -1241,7 +1415,7 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
         hvf[0] = sm.h[hs].V[0][lane];
         hvf[1] = sm.h[hs].V[1][lane];
         lds_wait_all();
-        if (lane == 0) lds_st(&sm.cons, c + 1);
+        if (lane == 0) lds_st(&sm.cons[j], (c >> 1) + 1);
         // O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T: lane (lg, lm) of tile mt
         // holds columns 4 lg .. 4 lg + 3 of the slice for token 16 mt + lm
         f32x4 ov[4];
@@ -1258,6 +1432,9 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
             ov[mt] = mfma16(hvf[0], mf[tri_base(mt)], ov[mt]);
             if (mt >= 2) ov[mt] = mfma16(hvf[1], mf[tri_base(mt) + 1], ov[mt]);
         }
+        // the products have read Q, M and s e^c: the next chunk's go out now
+        asm volatile("" : "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));
+        load(c + 2);
         const int rows = min(kChunk, x.len - c * kChunk);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
@@ -1278,12 +1455,6 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
                 *dst = pk;
             }
         }
-#pragma unroll
-        for (int f = 0; f < 16; ++f) qf[f] = qn[f];
-#pragma unroll
-        for (int f = 0; f < kTri; ++f) mf[f] = mn[f];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) es[mt] = en[mt];
     }
 }
 
@@ -1328,11 +1499,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
         chunks_before<kScanThreads>(a.cu, a.T, a.total, x.seq, sm.red));
     x.nch = seq_chunks_bounded(a.cu, a.T, a.total, x.seq, x.chunk0, a.nch_bound);
     if (tid == 0) {
-        lds_st(&sm.fillA, 0);
+        lds_st(&sm.fillC, 0);
+        lds_st(&sm.fillP, 0);
         lds_st(&sm.uready, 0);
-        lds_st(&sm.freeA, 0);
+        lds_st(&sm.freeC, 0);
         lds_st(&sm.ready, 0);
-        lds_st(&sm.cons, 0);
+        lds_st(&sm.cons[0], 0);
+        lds_st(&sm.cons[1], 0);
+        lds_st(&sm.dvready, 0);
+        lds_st(&sm.lodone, 0);
+        lds_st(&sm.scdone, 0);
         lds_st(&sm.abort, 0);
     }
     __syncthreads();
@@ -1340,7 +1516,17 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     switch (wave) {
         case 0: run_chain<kDbg>(sm, a, w, x, lane); break;
         case 1: run_producer<kRaw>(sm, a, w, x, lane); break;
-        case 2: run_output<kRaw>(sm, a, w, x, lane); break;
+        case 2: run_output<kRaw>(sm, a, w, x, 0, lane); break;
+        case 3: run_output<kRaw>(sm, a, w, x, 1, lane); break;
+        case 4:
+            // lo helper on the chain's SIMD; the debug build does that work
+            // in the chain, so it marks every chunk done at once
+            if (kDbg) {
+                if (tid == 256) lds_st(&sm.lodone, 1 << 30);
+            } else {
+                run_lo_helper(sm, a, w, x, lane);
+            }
+            break;
         default: run_loader(sm, a, w, x, lane); break;
     }
 }
