@@ -1091,10 +1091,11 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // Hand-off slot c % kHand is free once the chunk that used it before,
-// c - kHand (same parity), has been read by its output wave.
+// c - kHand (same parity), has been read by its output wave.  Loads without
+// a branch, so it can share one LDS round trip with other counter loads.
 __device__ inline bool slot_free(const ScanSmem& sm, int c) {
-    const int prev = c - kHand;
-    return prev < 0 || lds_ld(&sm.cons[prev & 1]) >= (prev >> 1) + 1;
+    const int need = c >= kHand ? ((c - kHand) >> 1) + 1 : 0;
+    return lds_ld(&sm.cons[c & 1]) >= need;
 }
 
 template <bool kDbg>
@@ -1143,32 +1144,45 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
     bool ok = true;
     for (int c = 0; c < x.nch; ++c) {
         const int hs = c % kHand;
-        ok = w.until([&] {
-            return lds_ld(&sm.fillC) >= c + 1 && lds_ld(&sm.uready) >= c + 1 && slot_free(sm, c) &&
-                   (kDbg || lds_ld(&sm.lodone) >= c - kLoSlots + 1);
-        });
-        if (!ok) break;
-        asm volatile("" ::: "memory");
         StageC& sc = sm.c[c % kRingC];
         StageP& sp = sm.p[c % kRingP];
-        // The step is laid out in issue order: every LDS read of a phase goes
-        // out before the phase's products, and the K^T reads of the state
-        // update go out behind the V_n products, so no product waits on a
-        // read issued just before it.
-        // (1) reads for V_n: U (accumulator init), -W, the gates
+        auto ready = [&] {   // every counter loaded, no short-circuit: one round trip
+            const bool f = lds_ld(&sm.fillC) >= c + 1, u = lds_ld(&sm.uready) >= c + 1;
+            const bool h = slot_free(sm, c);
+            const bool l = kDbg || lds_ld(&sm.lodone) >= c - kLoSlots + 1;
+            return f & u & h & l;
+        };
+        // (1) reads for V_n: U (accumulator init), -W, the gates.  They go
+        // out together with the counter reads, before the counters are
+        // known: a wave's LDS operations complete in order, so when the
+        // counters say the chunk is there, these reads saw it; otherwise
+        // the wave waits and reads again.  The usual case costs one LDS
+        // round trip instead of two.
         f32x4 Vn[4], dec[4];
         half8 wf[16];
+        float c63;
+        auto read_operands = [&] {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) Vn[mt] = sp.U[mt][lane];
+            for (int mt = 0; mt < 4; ++mt) Vn[mt] = sp.U[mt][lane];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+            for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) wf[mt * 4 + kb] = sc.W[mt * 4 + kb][lane];
+                for (int mt = 0; mt < 4; ++mt) wf[mt * 4 + kb] = sc.W[mt * 4 + kb][lane];
+            }
+            c63 = sp.gates[kGC63];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                dec[mt] = *reinterpret_cast<const f32x4*>(&sp.gates[kGDec + 16 * mt + 4 * lg]);
+        };
+        const bool early = ready();
+        asm volatile("" ::: "memory");
+        read_operands();
+        if (!early) {
+            ok = w.until(ready);
+            if (!ok) break;
+            asm volatile("" ::: "memory");
+            read_operands();
         }
-        const float c63 = sp.gates[kGC63];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            dec[mt] = *reinterpret_cast<const f32x4*>(&sp.gates[kGDec + 16 * mt + 4 * lg]);
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of the products
         if (kDbg) {
