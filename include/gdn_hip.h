@@ -40,6 +40,21 @@ extern "C" {
  * serves dump_debug = 0 and 1. */
 size_t deltanet_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int chunk_size);
 
+/* Allocation-free deltanet_chunk_prefill (dump_debug = 0): the workspace is
+ * a 48 MiB device array the library holds per GPU until the process ends,
+ * so the call allocates nothing (no hipMalloc, no allocating library call).
+ * No counterpart in the reference: it is for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops.  Every call on one GPU
+ * shares that array, so calls that overlap on one GPU (two streams, say)
+ * race; calls in one stream do not.  A call whose live workspace exceeds the
+ * array (more than 733 chunk-heads, e.g. T > 1408 at HV = 32) returns
+ * hipErrorInvalidValue before any launch. */
+hipError_t deltanet_chunk_prefill_noalloc(const void* q, const void* k, const void* v,
+                                          const float* g, const float* beta, void* o,
+                                          const float* initial_state, float* final_state, int B,
+                                          int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                          hipStream_t stream);
+
 /* Workspace bytes for dump_debug = 0 only (no counterpart in the reference,
  * whose size always includes its debug regions): a 256-byte header with the
  * status word, then 12 KB per (chunk, v-head). */

@@ -54,6 +54,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 namespace gdn {
 namespace {
@@ -1856,4 +1857,57 @@ extern "C" hipError_t deltanet_chunk_prefill_l2norm(
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
     return launch_prefill(in, 1, o, initial_state, final_state, nullptr, B, T, B * T, HV, HQK, nc,
                           workspace, workspace_bytes, stream, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free prefill: the workspace is a file-scope device array.
+// ---------------------------------------------------------------------------
+// 48 MiB per GPU that loads the library, held until the process ends: the
+// live workspace of up to (48 MiB - 256 B) / 67 KB = 733 chunk-heads, e.g.
+// T <= 1408 at HV = 32 (22 chunks).
+constexpr size_t kNoAllocScratchBytes = size_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The array's device address on the current device, looked up once per
+// device: in host code `scratch` names a host-side stand-in, never the
+// device memory.
+hipError_t noalloc_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t deltanet_chunk_prefill_noalloc(const void* q, const void* k, const void* v,
+                                                     const float* g, const float* beta, void* o,
+                                                     const float* initial_state,
+                                                     float* final_state, int B, int T, int HV,
+                                                     int HQK, int DK, int DV, int chunk_size,
+                                                     hipStream_t stream) {
+    if (!dims_ok(HV, HQK, DK, DV, chunk_size) || B <= 0 || T < 0) return hipErrorInvalidValue;
+    if (final_state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    if (WsLayout(nc * HV).live > kNoAllocScratchBytes) return hipErrorInvalidValue;   // too large
+    void* ws = nullptr;
+    const hipError_t e = noalloc_scratch(&ws);
+    if (e != hipSuccess) return e;
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
+                          T, B * T, HV, HQK, nc, ws, kNoAllocScratchBytes, stream, 0);
 }
