@@ -72,6 +72,26 @@ __device__ __forceinline__ half8 cat8(half4 lo, half4 hi) {
     return r;
 }
 
+// Two D-layout tiles a, b as an fp16 hi / lo pair of one packed operand:
+// hi = fp16(x), lo = fp16(x - hi), the residual taken from the packed hi bits
+// themselves.  Left alone, the compiler may form the two uses of hi
+// differently when x is a product: the operand as fp16(fp32(p)) (rounded
+// twice) and the residual's copy with a mixed-precision FMA, fp16(p)
+// (rounded once).  Next to an fp16 rounding midpoint those differ by one ulp,
+// and hi + lo is then one ulp of hi off.  x - hi is exact in fp32.
+__device__ __forceinline__ void split_hilo8(f32x4 a, f32x4 b, half8& hi, half8& lo) {
+    half8 h = cat8(to_half4(a), to_half4(b));
+    asm volatile("" : "+v"(h));
+    f32x4 ra, rb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ra[i] = a[i] - (float)h[i];
+        rb[i] = b[i] - (float)h[4 + i];
+    }
+    hi = h;
+    lo = cat8(to_half4(ra), to_half4(rb));
+}
+
 __device__ __forceinline__ f32x4 zero4() {
     f32x4 z = {0.f, 0.f, 0.f, 0.f};
     return z;

@@ -712,15 +712,10 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                 if (c0 + e == r) t0[e] -= 1.f;
                 if (c0 + 16 + e == r) t1[e] -= 1.f;
             }
-            const half4 h0 = to_half4(t0), h1 = to_half4(t1);
-            f32x4 l0, l1;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                l0[e] = t0[e] - (float)h0[e];
-                l1[e] = t1[e] - (float)h1[e];
-            }
-            tdst[(tri_base(mt) + kb) * 64 + lane] = cat8(h0, h1);
-            ldst[(tri_base(mt) + kb) * 64 + lane] = cat8(to_half4(l0), to_half4(l1));
+            half8 hi, lo;
+            split_hilo8(t0, t1, hi, lo);
+            tdst[(tri_base(mt) + kb) * 64 + lane] = hi;
+            ldst[(tri_base(mt) + kb) * 64 + lane] = lo;
         }
     }
 
@@ -1046,17 +1041,7 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
         }
         half8 xh[2], xl[2];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const half4 h0 = to_half4(X[2 * kb]), h1 = to_half4(X[2 * kb + 1]);
-            f32x4 r0, r1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                r0[i] = X[2 * kb][i] - (float)h0[i];
-                r1[i] = X[2 * kb + 1][i] - (float)h1[i];
-            }
-            xh[kb] = cat8(h0, h1);
-            xl[kb] = cat8(to_half4(r0), to_half4(r1));
-        }
+        for (int kb = 0; kb < 2; ++kb) split_hilo8(X[2 * kb], X[2 * kb + 1], xh[kb], xl[kb]);
         f32x4 U[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
