@@ -227,9 +227,15 @@ __device__ __forceinline__ bf16x8 tr_pair_bf16x8(s16x4 lo, s16x4 hi) {
 }
 
 // Row pieces of a 64 x 128 16-bit tile in LDS: piece p (8 elements) of row r
-// sits at 16 r + (p ^ (r & 15)), so both 16-byte row-piece reads and the
-// transposing reads below are free of bank conflicts.
-__device__ __forceinline__ int row_slot(int r, int p) { return 16 * r + (p ^ (r & 15)); }
+// sits at slot 16 r + (p ^ sw(r)), sw(r) = the two 2-bit halves of r % 16
+// swapped.  sw is a bijection on r % 16, so 16 consecutive rows' piece p and
+// one row's 16 pieces each fill 16 distinct slots; and for 4 consecutive rows
+// (r % 4 = 0..3) x 4 consecutive pieces (p % 4 = 0..3) -- a 16-lane group of
+// the transposing reads below -- the high bits of p ^ sw(r) follow the row
+// and the low bits the piece, so those 16 reads hit 16 distinct slots too:
+// all three patterns are free of bank conflicts.
+__device__ __forceinline__ int row_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int row_slot(int r, int p) { return 16 * r + (p ^ row_swz(r)); }
 
 // Transposed operand of rows tile t (0..7) and token k-block kb (0..1) of a
 // 64-token tile stored as above: lane (g, m) receives rows
@@ -945,10 +951,10 @@ __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
         StageC& st = sm.c[c % kRingC];
         const int t0 = x.tok_base + c * kChunk, rows = rows_of(c);
         // K rows: slot s = 64 i + lane -> row s / 16, stored piece s % 16,
-        // which is source piece (s % 16) ^ (row % 16)
+        // which is source piece (s % 16) ^ row_swz(row)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int s = 64 * i + lane, r = s >> 4, p = (s & 15) ^ (r & 15);
+            const int s = 64 * i + lane, r = s >> 4, p = (s & 15) ^ row_swz(r);
             const int rr = min(r, rows - 1);
             lds_dma16(a.krows + ((size_t)(t0 + rr) * a.HK + x.hk) * kDK + 8 * p, &st.K[64 * i]);
         }
