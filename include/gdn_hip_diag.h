@@ -1,8 +1,9 @@
 /*
  * Diagnostic entry points of libgdn_hip.so: per-kernel timing, a bounded-wait
- * test hook and the host mirror of the varlen chunk bookkeeping.  None is part
- * of the drop-in boundary (include/gdn_hip.h) and none has a counterpart in
- * the reference; benchmarks and tests use them.  Conventions as in gdn_hip.h.
+ * test hook, the host mirror of the varlen chunk bookkeeping and an HBM
+ * streaming probe.  None is part of the drop-in boundary (include/gdn_hip.h)
+ * and none has a counterpart in the reference; benchmarks and tests use them.
+ * Conventions as in gdn_hip.h.
  */
 #ifndef GDN_HIP_DIAG_H_
 #define GDN_HIP_DIAG_H_
@@ -64,6 +65,15 @@ hipError_t deltanet_chunk_prefill_spin(const void* q, const void* k, const void*
 int deltanet_varlen_chunk_map(const int32_t* cu_seqlens, int num_seqs, int total_tokens,
                               int32_t* seq_first_chunk, int32_t* seq_chunk_count,
                               int32_t* seq_first_token, int32_t* seq_token_count);
+
+/* HBM streaming probe (benchmarks only): kind 0 reads a and b and writes
+ * c = a ^ b, `bytes` each (three streams, the gated RMSNorm's pattern);
+ * kind 1 reads and rewrites c in place (the decode state's pattern).
+ * nontemporal != 0 uses non-temporal loads and stores.  `blocks` work-groups
+ * of 256 threads stride over the 16-byte vectors.  bytes must be a nonzero
+ * multiple of 16, otherwise hipErrorInvalidValue. */
+hipError_t gdn_stream_probe(int kind, int nontemporal, const void* a, const void* b, void* c,
+                            size_t bytes, int blocks, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -22,7 +22,8 @@ OUT = PKG_ROOT / "gdn_hip"
 INCLUDE = REPO / "include"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ["gdn_prefill.hip", "gdn_decode.hip", "gated_rmsnorm.hip", "causal_conv1d.hip"]
+HIP_SOURCES = ["gdn_prefill.hip", "gdn_decode.hip", "gated_rmsnorm.hip", "causal_conv1d.hip",
+               "stream_probe.hip"]
 LIB_NAME = "libgdn_hip.so"
 EXT_NAME = "deltanet_chunk_hip"
 

@@ -61,6 +61,7 @@ _PROTOS = {
                                                c_int, hipStream_t]),
     "gdn_causal_conv1d_fwd": (hipError_t, [vp, vp, vp, vp] + [c_int] * 4 + [c_int64] * 4 +
                               [c_int] * 3 + [hipStream_t]),
+    "gdn_stream_probe": (hipError_t, [c_int, c_int, vp, vp, vp, c_size_t, c_int, hipStream_t]),
     "gdn_causal_conv1d_update": (hipError_t, [vp, vp, vp, vp, vp] + [c_int] * 5 + [c_int64] * 8 +
                                  [c_int] * 3 + [hipStream_t]),
 }
