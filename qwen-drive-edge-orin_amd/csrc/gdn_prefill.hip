@@ -75,14 +75,15 @@ __host__ __device__ constexpr int tri_base(int mt) { return mt < 3 ? mt : 4; }
 //   W         -W, row tile mt, k-block kb   16 fragments            16 KB
 //   gates     beta, d = e^{c63 - c}, s e^c, c63                      1 KB
 //   Q         Q rows as fp16 fragments, per (chunk, k-head)          16 KB
-//   Kn        normalised k rows (raw-input entries), [token][HK][128] bf16
+//   KT        K^T as bf16 A-operand fragments of the state update, per
+//             (chunk, k-head): tile t = dk block, k-block kb = tokens        16 KB
 // A 256-byte header in front holds the status word.
 constexpr size_t kFrag = 64 * 16;                      // one fragment: 1 KB
 constexpr size_t kTriBytes = (size_t)kTri * kFrag;     // 6 KB
 constexpr size_t kWBytes = 16 * kFrag;                 // 16 KB
 constexpr size_t kGateBytes = 1024;
 constexpr size_t kQBytes = 16 * kFrag;                 // 16 KB
-constexpr size_t kKnBytes = (size_t)kChunk * kDK * 2;  // 16 KB of k rows per chunk-head bound
+constexpr size_t kKTBytes = 16 * kFrag;                // 16 KB
 constexpr size_t kHeaderBytes = 256;
 
 // gates record: float offsets
@@ -95,7 +96,7 @@ struct Workspace {
     half8* W;           // -W fragments [chunk-head][mt * 4 + kb][64]
     float* gates;       // [chunk-head][256]
     half8* Q;           // Q fragments [chunk * HK + hk][mt * 4 + kb][64]
-    uint16_t* Kn;       // normalised k rows (raw-input entries) [token][HK][128]
+    u32x4* KT;          // K^T bf16 fragments [chunk * HK + hk][t * 2 + kb][64]
     unsigned* status;   // bit 0: a bounded wait gave up
     float* dbgT;        // optional [chunk-head][64][64]: T = (I - A)^-1
     float* dbgA;        // optional: A
@@ -110,7 +111,7 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 // Byte layout of the workspace for `nch` chunk-heads.  The debug regions stay
 // last: the torch binding finds them from the end.
 struct WsLayout {
-    size_t ti, tilo, m, w, gates, q, kn, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
+    size_t ti, tilo, m, w, gates, q, kt, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
     __host__ explicit WsLayout(size_t nch) {
         size_t off = kHeaderBytes;
         ti = off;    off += align256(nch * kTriBytes);
@@ -119,7 +120,7 @@ struct WsLayout {
         w = off;     off += align256(nch * kWBytes);
         gates = off; off += align256(nch * kGateBytes);
         q = off;     off += align256(nch * kQBytes);
-        kn = off;    off += align256(nch * kKnBytes);
+        kt = off;    off += align256(nch * kKTBytes);
         live = off;
         dbgT = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgA = off;  off += align256(nch * kChunk * kChunk * 4);
@@ -462,8 +463,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     }
 
     // ---- K rows -> fp16 into LDS (normalised first for raw inputs); rows
-    // past the chunk's end are zeroed.  For raw inputs the first v-head of
-    // the GQA group also stores the normalised bf16 rows for the scan.
+    // past the chunk's end are zeroed.
     const bool writer = member == 0;
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
@@ -479,9 +479,6 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) x[e] = (float)(__bf16)(x[e] * inv);
-            if (writer && r < rows)
-                *reinterpret_cast<u32x4*>(ws.Kn + ((size_t)(tok0 + r) * HK + hk) * kDK + 8 * p) =
-                    f32x8_to_bf16x8(x);
         }
         u32x4 v = __builtin_bit_cast(u32x4, f32x8_to_half8(x));
         if (r >= rows) v = u32x4{0u, 0u, 0u, 0u};
@@ -734,6 +731,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     {
         const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sm.K);
         half8 kt[2][2];
+        u32x4* ktdst = ws.KT + ((size_t)cid * HK + hk) * (16 * 64);
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
@@ -741,6 +739,14 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                 s16x4 x0, x1;
                 kt_reads(kbase, 2 * wave + tt, kb, lane, x0, x1);
                 kt[tt][kb] = tr_pair_half8(x0, x1);
+                // the scan's K^T operand of tile 2 w + tt, k-block kb (bf16:
+                // the fp16 values convert back exactly, they were bf16)
+                if (writer) {
+                    bf16x8 kb16;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) kb16[e] = (__bf16)(float)kt[tt][kb][e];
+                    ktdst[((2 * wave + tt) * 2 + kb) * 64 + lane] = __builtin_bit_cast(u32x4, kb16);
+                }
             }
         }
         f32x4 bec[2][2];   // beta e^c at columns 32 kb + 4 g (+16) .. + 3
@@ -785,35 +791,37 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
 // produces tile t is two transposing LDS reads of K rows.
 //
 //   chain     wave 0: V_n = U + (-W) S16 (16 fp16 MFMA), d V_n -> bf16 hi / lo,
-//             S' = e^{c63} S + K^T hi (16 bf16 MFMA), Sc += K^T (sigma lo)
-//             (16 bf16 MFMA, off the serial path: sigma = e^{sum of the
-//             later chunks' c63} pre-applies the decay the lo part would
-//             see, so Sc needs no per-chunk scaling).  Wave 4, on the same
-//             SIMD, exits at once.
+//             S' = e^{c63} S + K^T hi (16 bf16 MFMA), then Sc <- e^{c63} Sc
+//             + K^T lo (16 bf16 MFMA) off the serial path: those products
+//             run in the matrix pipe while the wave hands off, publishes and
+//             reads the next chunk's operands.
 //   producer  wave 1: U = beta V + (T - I)(beta V) with the product as
 //             hi/hi + hi/lo + lo/hi fp16 MFMAs (18), into ring P.
 //   output    waves 2 and 3, chunks of even and odd index:
 //             O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T, with Q, M and s e^c
 //             loaded to registers as soon as the wave's previous chunk has
 //             read them, two chain steps before they are needed.
-//   loader    wave 5 (on the producer's SIMD): direct-to-LDS loads of K rows
-//             and -W into ring C (3 stages, 32 KB each) and of V and the
-//             gates record into ring P (5 stages, 7 KB each, filled two chunks
-//             ahead of ring C), plus L2 warm-up loads of the K rows and -W
-//             two chunks ahead of their ring-C loads.
+//   prefetch  wave 4: L2 warm-up loads kPf chunks ahead of the chain.
+//   loaders   waves 6 and 5, chunks of even and odd index: direct-to-LDS
+//             loads of chunk c's K rows and -W into ring C (3 stages, 32 KB
+//             each) and of chunk c + 1's V and gates record into ring P (4
+//             stages, 7 KB each).  Each loader has one chunk in flight and
+//             publishes it as soon as it lands, so the two keep two chunks in
+//             flight without one's wait for a free stage holding back the
+//             other's publication.
 // ---------------------------------------------------------------------------
 constexpr int kRingC = 3;     // chain operand stages (K rows, -W)
 constexpr int kRingP = 4;     // producer stages (V, gates, U)
 constexpr int kLeadP = 1;     // ring P is filled this many chunks ahead of ring C
-constexpr int kLoSlots = 2;   // chain -> lo-helper hand-off slots
 constexpr int kHand = 4;      // chain -> output hand-off slots
-constexpr int kScanWaves = 6;
+constexpr int kLoSlots = 2;   // chain -> lo-helper hand-off slots
+constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
 static_assert(kRingP >= kRingC + kLeadP, "ring P must hold the chunks ring C and the lead span");
 static_assert(kHand % 2 == 0, "a hand-off slot is reused by a chunk of the same parity");
 
 struct StageC {
-    u32x4 K[kChunk * 16];   // bf16 K rows, row_slot layout
+    u32x4 KT[16][64];       // K^T bf16 fragments (t * 2 + kb)
     half8 W[16][64];        // -W fragments (mt * 4 + kb)
 };
 
@@ -830,7 +838,7 @@ struct Hand {
 
 struct LoHand {
     f32x4 d[4][64];         // d o V_n (fp32, D layout per row tile)
-    float sig;              // sigma of the chunk
+    float gam;              // e^{c63} of the chunk
     float pad_[63];
 };
 
@@ -839,14 +847,14 @@ struct ScanSmem {
     StageP p[kRingP];
     Hand h[kHand];
     LoHand lo[kLoSlots];   // after the last chunk: the helper's Sc (8 KB)
-    int fillC;       // chunks whose ring-C loads have landed (loader)
-    int fillP;       // chunks whose ring-P loads have landed (loader)
+    int fill[2];     // per loader: chunks of its parity whose ring-C loads (and the next
+                     // chunk's ring-P loads) have landed
     int uready;      // chunks whose U is in ring P (producer)
     int freeC;       // chunks whose ring-C and ring-P stages the chain has finished reading
     int ready;       // chunks whose hand-off slot the chain has written
     int cons[2];     // per output wave: chunks of its parity whose hand-off slot it has read
     int dvready;     // chunks whose d o V_n the chain has handed to the helper
-    int lodone;      // chunks whose lo part the helper has accumulated
+    int lodone;      // chunks whose lo slot the helper has read
     int scdone;      // the helper's Sc is in the lo slots
     int abort;       // a bounded wait ran out: every wave stops
     int seqsel;
@@ -904,7 +912,6 @@ struct ScanArgs {
     const float* s0;
     float* sf;
     const int32_t* cu;
-    const uint16_t* krows;   // K rows for the state update: the input k, or the normalised Kn
     int N, T, total, HV, HK, nch_bound;
     unsigned spin;
 };
@@ -922,16 +929,14 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
 constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
 static_assert(vmcnt_imm(16) == 0x4F70 && vmcnt_imm(0) == 0x0F70, "s_waitcnt encoding");
 
-// Loader step c issues one group of direct-to-LDS loads: ring P for chunk
-// c + kLeadP (V: 2, gates: 1) and ring C for chunk c (K rows: 16, -W: 16).
+// Loader j (0 or 1) takes the chunks c of parity j: it issues one group of
+// direct-to-LDS loads, ring C for chunk c (K rows: 16, -W: 16) and ring P for
+// chunk c + kLeadP (V: 2, gates: 1), waits for the group and publishes it.
 // Past the sequence's end the ring-P index is clamped, so every group holds
-// the same number of loads.
-constexpr int kGroupLoads = 3 + 32;
-constexpr unsigned kVmcntGroup = vmcnt_imm(kGroupLoads);
-constexpr unsigned kVmcntRoom = vmcnt_imm(63 - kGroupLoads);   // at most 63 in flight
-
+// the same number of loads.  Loader 0 also loads ring P's lead chunks
+// first, published with its first group.
 __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
-                           int lane) {
+                           int j, int lane) {
     auto rows_of = [&](int c) { return min(kChunk, x.len - c * kChunk); };
     auto ch_of = [&](int c) { return (size_t)(x.chunk0 + c) * a.HV + x.hv; };
     auto issue_p = [&](int cp) {
@@ -949,54 +954,29 @@ __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
     };
     auto issue_c = [&](int c) {
         StageC& st = sm.c[c % kRingC];
-        const int t0 = x.tok_base + c * kChunk, rows = rows_of(c);
-        // K rows: slot s = 64 i + lane -> row s / 16, stored piece s % 16,
-        // which is source piece (s % 16) ^ row_swz(row)
+        const u32x4* ksrc = a.ws.KT + ((size_t)(x.chunk0 + c) * a.HK + x.hk) * (16 * 64) + lane;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int s = 64 * i + lane, r = s >> 4, p = (s & 15) ^ row_swz(r);
-            const int rr = min(r, rows - 1);
-            lds_dma16(a.krows + ((size_t)(t0 + rr) * a.HK + x.hk) * kDK + 8 * p, &st.K[64 * i]);
-        }
+        for (int f = 0; f < 16; ++f) lds_dma16(ksrc + f * 64, &st.KT[f][0]);
         const half8* wsrc = a.ws.W + ch_of(c) * (16 * 64) + lane;
 #pragma unroll
         for (int f = 0; f < 16; ++f) lds_dma16(wsrc + f * 64, &st.W[f][0]);
     };
+    // an empty sequence has no chunk to load (issue_p would form chunk -1)
     if (x.nch <= 0) return;
-    // prologue: ring P for chunks 0 .. kLeadP - 1
-    for (int c = 0; c < kLeadP; ++c) issue_p(c);
-    vm_wait_all();
-    if (lane == 0) lds_st(&sm.fillP, kLeadP);
-    for (int c = 0; c < x.nch; ++c) {
-        // ring-C stage c % kRingC held chunk c - kRingC (read by the chain
-        // and the lo helper); ring-P stage (c + kLeadP) % kRingP held chunk
-        // c + kLeadP - kRingP <= c - kRingC
-        if (!w.until([&] {
-                return min(lds_ld(&sm.freeC), lds_ld(&sm.lodone)) >= c - kRingC + 1;
-            })) {
-            vm_wait_all();   // no load may land in LDS after the group ends
-            return;
-        }
+    if (j == 0) {
+        for (int c = 0; c < kLeadP; ++c) issue_p(c);
+    }
+    for (int c = j; c < x.nch; c += 2) {
+        // ring-C stage c % kRingC held chunk c - kRingC; ring-P stage
+        // (c + kLeadP) % kRingP held chunk c + kLeadP - kRingP <= c - kRingC
+        if (!w.until([&] { return lds_ld(&sm.freeC) >= c - kRingC + 1; })) break;
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(kVmcntRoom);
         issue_p(c + kLeadP);
         issue_c(c);
-        if (c > 0) {
-            // group c - 1 has landed (group c may be in flight)
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_waitcnt(kVmcntGroup);
-            asm volatile("" ::: "memory");
-            if (lane == 0) {
-                lds_st(&sm.fillC, c);
-                lds_st(&sm.fillP, c + kLeadP);
-            }
-        }
+        vm_wait_all();
+        if (lane == 0) lds_st(&sm.fill[j], (c >> 1) + 1);
     }
-    vm_wait_all();
-    if (lane == 0) {
-        lds_st(&sm.fillC, x.nch);
-        lds_st(&sm.fillP, x.nch + kLeadP);
-    }
+    vm_wait_all();   // no load may land in LDS after the group ends
 }
 
 template <int kRaw>
@@ -1029,7 +1009,10 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
     load_t(0, th, tl);
     for (int c = 0; c < x.nch; ++c) {
         load_t(c + 1, nh, nl);
-        if (!w.until([&] { return lds_ld(&sm.fillP) >= c + 1; })) return;
+        // ring P of chunk c landed with loader group c - kLeadP (chunk 0's
+        // lead with loader 0's first group)
+        const int lc = max(c - kLeadP, 0);
+        if (!w.until([&] { return lds_ld(&sm.fill[lc & 1]) >= (lc >> 1) + 1; })) return;
         asm volatile("" ::: "memory");
         StageP& st = sm.p[c % kRingP];
         // X = beta V: lane (g, n) of tile mt holds tokens 16 mt + 4 g + i of
@@ -1098,9 +1081,9 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
     auto dk_of = [&](int t, int i) { return 32 * (t >> 1) + 8 * lg + 4 * (t & 1) + i; };
     const size_t sbase = ((size_t)x.seq * a.HV + x.hv) * kDK * kDV + col;
 
-    // Sd (debug builds only): the lo part without the sigma pre-scaling,
-    // decayed every chunk, so S + Sd is the state at each chunk's start
-    f32x4 S[8], Sc[8], Sd[8];
+    // S: the state's bf16-hi accumulation; Sc: the lo part, decayed every
+    // chunk, so S + Sc is the state at each chunk's start
+    f32x4 S[8], Sc[8];
     if (a.s0) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -1112,22 +1095,7 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
         for (int t = 0; t < 8; ++t) S[t] = zero4();
     }
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        Sc[t] = zero4();
-        Sd[t] = zero4();
-    }
-
-    // remaining log-decay after each chunk: rem = sum of c63 over the later
-    // chunks of this sequence; starts as the total
-    float rem = 0.f;
-    for (int j0 = 0; j0 < x.nch; j0 += 64) {
-        const int j = j0 + lane;
-        float v = 0.f;
-        if (j < x.nch) v = a.ws.gates[((size_t)(x.chunk0 + j) * a.HV + x.hv) * (kGateBytes / 4) + kGC63];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        rem += v;
-    }
+    for (int t = 0; t < 8; ++t) Sc[t] = zero4();
 
     half8 S16[4];
 #pragma unroll
@@ -1139,7 +1107,8 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
         StageC& sc = sm.c[c % kRingC];
         StageP& sp = sm.p[c % kRingP];
         auto ready = [&] {   // every counter loaded, no short-circuit: one round trip
-            const bool f = lds_ld(&sm.fillC) >= c + 1, u = lds_ld(&sm.uready) >= c + 1;
+            const bool f = lds_ld(&sm.fill[c & 1]) >= (c >> 1) + 1;
+            const bool u = lds_ld(&sm.uready) >= c + 1;
             const bool h = slot_free(sm, c);
             const bool l = kDbg || lds_ld(&sm.lodone) >= c - kLoSlots + 1;
             return f & u & h & l;
@@ -1182,7 +1151,7 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) dst[(size_t)dk_of(t, i) * kDV] = S[t][i] + Sd[t][i];
+                for (int i = 0; i < 4; ++i) dst[(size_t)dk_of(t, i) * kDV] = S[t][i] + Sc[t][i];
             }
         }
         // (2) V_n = U + (-W) S16: row tile mt (tokens), k-block kb (dk)
@@ -1191,31 +1160,20 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) Vn[mt] = mfma16(wf[mt * 4 + kb], S16[kb], Vn[mt]);
         }
-        // (3) K^T operands of the state update (32 transposing reads)
-        const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sc.K);
+        // (3) K^T operands of the state update (16 fragment reads)
         bf16x8 kt[8][2];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                s16x4 x0, x1;
-                kt_reads(kbase, t, kb, lane, x0, x1);
-                kt[t][kb] = tr_pair_bf16x8(x0, x1);
-            }
+            for (int kb = 0; kb < 2; ++kb) kt[t][kb] = __builtin_bit_cast(bf16x8, sc.KT[t * 2 + kb][lane]);
         }
         // (4) decay of the state while the V_n products run; S at the
         // chunk's start goes to the hand-off slot
         const float gam = __builtin_amdgcn_exp2f(c63 * kLog2e);
-        rem -= c63;
-        const float sig = __builtin_amdgcn_exp2f(rem * kLog2e);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) sm.h[hs].S[kb][lane] = S16[kb];
 #pragma unroll
         for (int t = 0; t < 8; ++t) S[t] = S[t] * gam;
-        if (kDbg) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) Sd[t] = Sd[t] * gam;
-        }
         // A wave issues in order: each product is followed by independent
         // VALU work and reads, so they run while the product is in the
         // matrix pipe instead of after all products.
@@ -1248,30 +1206,26 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        // (6) d o V_n (and sigma) to the lo helper on this SIMD, which adds
-        // K^T (sigma lo) to its Sc off the serial path (the debug build keeps
-        // that work here, with Sd beside it)
-        if (!kDbg) {
+        // (6) d o V_n and the decay to the lo helper (SIMD 3), which adds K^T
+        // lo to its decayed Sc off the serial path; published with the
+        // chunk's other counters.  The debug build does that work here.
+        if constexpr (!kDbg) {
             LoHand& lh = sm.lo[c % kLoSlots];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) lh.d[mt][lane] = dv[mt];
-            if (lane == 0) lh.sig = sig;
-            lds_wait_all();
-            if (lane == 0) lds_st(&sm.dvready, c + 1);
+            if (lane == 0) lh.gam = gam;
         }
-        __builtin_amdgcn_sched_barrier(0);
         // (7) S' = e^{c63} S + K^T hi.  Issue order is fixed piece by piece
-        // (the wave issues in order): the lo-part VALU (debug build) and the
-        // S16 and V_n conversions are spread between the products.
-        u32x4 lw[2], uw[2];
+        // (the wave issues in order): the S16 and V_n conversions (and, in
+        // the debug build, the lo residuals) are spread between the products.
+        u32x4 lw[2];
         auto lo_pair = [&](int kb, int q) {   // q = 2 h + p: one packed pair
             const int h = q >> 1, p = q & 1;
             const f32x4& d = dv[2 * kb + h];
             const uint32_t hp = hw[kb][q];
             const float r0 = d[2 * p] - __uint_as_float(hp << 16);
             const float r1 = d[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
-            lw[kb][q] = pack_bf16x2(r0 * sig, r1 * sig);
-            uw[kb][q] = pack_bf16x2(r0, r1);
+            lw[kb][q] = pack_bf16x2(r0, r1);
         };
         half8 vh[2];
 #pragma unroll
@@ -1284,20 +1238,19 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
                 if (kb == 0 && t < 2) vh[t] = cat8(to_half4(Vn[2 * t]), to_half4(Vn[2 * t + 1]));
                 if (kb == 1 && (t & 1))
                     S16[t >> 1] = cat8(to_half4(S[t - 1]), to_half4(S[t]));
+                if (kDbg && kb == 1) Sc[t] = Sc[t] * gam;
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (kDbg) {
+        if constexpr (kDbg) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
+                for (int t = 0; t < 8; ++t)
                     Sc[t] = mfma16_bf16(kt[t][kb], __builtin_bit_cast(bf16x8, lw[kb]), Sc[t]);
-                    Sd[t] = mfma16_bf16(kt[t][kb], __builtin_bit_cast(bf16x8, uw[kb]), Sd[t]);
-                }
             }
         }
-        // (7) hand-off of V_n (fp16) for the output
+        // (8) hand-off of V_n (fp16) for the output
         sm.h[hs].V[0][lane] = vh[0];
         sm.h[hs].V[1][lane] = vh[1];
         __builtin_amdgcn_sched_barrier(0);
@@ -1305,6 +1258,7 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
         if (lane == 0) {
             lds_st(&sm.ready, c + 1);
             lds_st(&sm.freeC, c + 1);
+            if (!kDbg) lds_st(&sm.dvready, c + 1);
         }
     }
     if (!ok) return;
@@ -1323,37 +1277,37 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
     }
 }
 
-// Lo helper (the chain's SIMD): Sc += K^T (sigma lo) per chunk, with d o V_n
-// from the chain split again into its bf16 hi part and the residual lo =
-// bf16(sigma (d o V_n - hi)), the same values the chain's hi part leaves out.
-// A single wave issues about half of its SIMD's MFMA rate, so these products
-// run beside the chain's instead of after them.  After the last chunk Sc goes
-// to the lo slots for the chain.
+// Lo helper (SIMD 3): Sc <- e^{c63} Sc + K^T lo per chunk, with d o V_n from
+// the chain split again into its bf16 hi part and the residual lo =
+// bf16(d o V_n - hi), the same values the chain's hi part leaves out.  The K^T
+// fragments come straight from global memory (the loaders have just brought
+// them into L2), one chunk ahead, so ring C never waits for this wave.  After
+// the last chunk Sc goes to the lo slots for the chain.
 __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                               int lane) {
+    if (x.nch <= 0) return;
     f32x4 Sc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) Sc[t] = zero4();
-    if (x.nch <= 0) return;
+    u32x4 kc[16], kn[16];
+    auto load_kt = [&](int c, u32x4 (&k)[16]) {
+        const int cc = min(c, x.nch - 1);
+        const u32x4* src = a.ws.KT + ((size_t)(x.chunk0 + cc) * a.HK + x.hk) * (16 * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < 16; ++f) k[f] = src[f * 64];
+    };
+    load_kt(0, kc);
     for (int c = 0; c < x.nch; ++c) {
+        load_kt(c + 1, kn);
         if (!w.until([&] { return lds_ld(&sm.dvready) >= c + 1; })) return;
         asm volatile("" ::: "memory");
         const LoHand& lh = sm.lo[c % kLoSlots];
         f32x4 d[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) d[mt] = lh.d[mt][lane];
-        const float sig = lh.sig;
-        const uint16_t* kbase = reinterpret_cast<const uint16_t*>(sm.c[c % kRingC].K);
-        bf16x8 kt[8][2];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                s16x4 x0, x1;
-                kt_reads(kbase, t, kb, lane, x0, x1);
-                kt[t][kb] = tr_pair_bf16x8(x0, x1);
-            }
-        }
+        const float gam = lh.gam;
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.lodone, c + 1);
         bf16x8 lo[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -1366,18 +1320,21 @@ __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, 
                     const uint32_t hp = pack_bf16x2(dd[2 * p], dd[2 * p + 1]);
                     const float r0 = dd[2 * p] - __uint_as_float(hp << 16);
                     const float r1 = dd[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
-                    lw[2 * h + p] = pack_bf16x2(r0 * sig, r1 * sig);
+                    lw[2 * h + p] = pack_bf16x2(r0, r1);
                 }
             }
             lo[kb] = __builtin_bit_cast(bf16x8, lw);
         }
 #pragma unroll
+        for (int t = 0; t < 8; ++t) Sc[t] = Sc[t] * gam;
+#pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) Sc[t] = mfma16_bf16(kt[t][kb], lo[kb], Sc[t]);
+            for (int t = 0; t < 8; ++t)
+                Sc[t] = mfma16_bf16(__builtin_bit_cast(bf16x8, kc[t * 2 + kb]), lo[kb], Sc[t]);
         }
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.lodone, c + 1);
+#pragma unroll
+        for (int f = 0; f < 16; ++f) kc[f] = kn[f];
     }
     // every chunk's slot has been read: Sc goes to the lo slots
     f32x4* dst = &sm.lo[0].d[0][0];
@@ -1505,8 +1462,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
         chunks_before<kScanThreads>(a.cu, a.T, a.total, x.seq, sm.red));
     x.nch = seq_chunks_bounded(a.cu, a.T, a.total, x.seq, x.chunk0, a.nch_bound);
     if (tid == 0) {
-        lds_st(&sm.fillC, 0);
-        lds_st(&sm.fillP, 0);
+        lds_st(&sm.fill[0], 0);
+        lds_st(&sm.fill[1], 0);
         lds_st(&sm.uready, 0);
         lds_st(&sm.freeC, 0);
         lds_st(&sm.ready, 0);
@@ -1519,21 +1476,22 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     }
     __syncthreads();
     const Waiter w{&sm.abort, a.ws.status, a.spin};
+    // Waves go to SIMDs round-robin (wave w on SIMD w % 4): the chain has
+    // SIMD 0 to itself (wave 4 exits at once); the loaders share SIMDs 1 and 2
+    // with the producer and an output wave, the lo helper SIMD 3 with the
+    // other output wave.
     switch (wave) {
         case 0: run_chain<kDbg>(sm, a, w, x, lane); break;
         case 1: run_producer<kRaw>(sm, a, w, x, lane); break;
         case 2: run_output<kRaw>(sm, a, w, x, 0, lane); break;
         case 3: run_output<kRaw>(sm, a, w, x, 1, lane); break;
-        case 4:
-            // lo helper on the chain's SIMD; the debug build does that work
-            // in the chain, so it marks every chunk done at once
-            if (kDbg) {
-                if (tid == 256) lds_st(&sm.lodone, 1 << 30);
-            } else {
-                run_lo_helper(sm, a, w, x, lane);
-            }
+        case 4: break;
+        case 5: run_loader(sm, a, w, x, 1, lane); break;
+        case 6: run_loader(sm, a, w, x, 0, lane); break;
+        default:
+            // the debug build does the lo helper's work in the chain
+            if constexpr (!kDbg) run_lo_helper(sm, a, w, x, lane);
             break;
-        default: run_loader(sm, a, w, x, lane); break;
     }
 }
 
@@ -1555,7 +1513,7 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     ws.W = reinterpret_cast<half8*>(base + L.w);
     ws.gates = reinterpret_cast<float*>(base + L.gates);
     ws.Q = reinterpret_cast<half8*>(base + L.q);
-    ws.Kn = reinterpret_cast<uint16_t*>(base + L.kn);
+    ws.KT = reinterpret_cast<u32x4*>(base + L.kt);
     ws.status = reinterpret_cast<unsigned*>(base);
     if (dump_debug) {
         ws.dbgT = reinterpret_cast<float*>(base + L.dbgT);
@@ -1590,7 +1548,6 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     sa.s0 = s0;
     sa.sf = sf;
     sa.cu = cu;
-    sa.krows = raw ? ws.Kn : in.k;
     sa.N = N;
     sa.T = T;
     sa.total = total_tokens;
