@@ -988,12 +988,14 @@ __device__ inline float v16_to_f32(uint32_t bits) {
 
 // Producer: U = beta V + (T - I)(beta V) per chunk into ring P.  With X =
 // beta V (fp32, D layout), the product is (T-I)_hi X_hi + (T-I)_hi X_lo +
-// (T-I)_lo X_hi on fp16 MFMA, accumulated onto X.
+// (T-I)_lo X_hi on fp16 MFMA, accumulated onto X.  The (T - I) fragments come
+// straight from global memory three chunks ahead, in three register sets
+// used in turn (a set is refilled right after its chunk's products have read
+// it, so no copy ever waits for a load in flight).
 template <int kRaw>
 __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                              int lane) {
     const int lg = lane >> 4, lm = lane & 15;
-    half8 th[kTri], tl[kTri], nh[kTri], nl[kTri];
     auto load_t = [&](int c, half8 (&h)[kTri], half8 (&l)[kTri]) {
         const int cc = min(c, x.nch - 1);
         const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
@@ -1005,14 +1007,11 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
             l[f] = pl[f * 64];
         }
     };
-    if (x.nch <= 0) return;
-    load_t(0, th, tl);
-    for (int c = 0; c < x.nch; ++c) {
-        load_t(c + 1, nh, nl);
+    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri]) -> bool {
         // ring P of chunk c landed with loader group c - kLeadP (chunk 0's
         // lead with loader 0's first group)
         const int lc = max(c - kLeadP, 0);
-        if (!w.until([&] { return lds_ld(&sm.fill[lc & 1]) >= (lc >> 1) + 1; })) return;
+        if (!w.until([&] { return lds_ld(&sm.fill[lc & 1]) >= (lc >> 1) + 1; })) return false;
         asm volatile("" ::: "memory");
         StageP& st = sm.p[c % kRingP];
         // X = beta V: lane (g, n) of tile mt holds tokens 16 mt + 4 g + i of
@@ -1044,15 +1043,24 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
                 U[mt] = mfma16(tl[f], xh[kb], U[mt]);
             }
         }
+        // the products have read this set: chunk c + 3's fragments go in
+        load_t(c + 3, th, tl);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) st.U[mt][lane] = U[mt];
         lds_wait_all();
         if (lane == 0) lds_st(&sm.uready, c + 1);
-#pragma unroll
-        for (int f = 0; f < kTri; ++f) {
-            th[f] = nh[f];
-            tl[f] = nl[f];
-        }
+        return true;
+    };
+    if (x.nch <= 0) return;
+    half8 t0h[kTri], t0l[kTri], t1h[kTri], t1l[kTri], t2h[kTri], t2l[kTri];
+    load_t(0, t0h, t0l);
+    load_t(1, t1h, t1l);
+    load_t(2, t2h, t2l);
+    // step() is false only when a bounded wait gave up
+    for (int c = 0; c < x.nch; c += 3) {
+        if (!step(c, t0h, t0l)) return;
+        if (c + 1 < x.nch && !step(c + 1, t1h, t1l)) return;
+        if (c + 2 < x.nch && !step(c + 2, t2h, t2l)) return;
     }
 }
 
@@ -1281,7 +1289,8 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
 // the chain split again into its bf16 hi part and the residual lo =
 // bf16(d o V_n - hi), the same values the chain's hi part leaves out.  The K^T
 // fragments come straight from global memory (the loaders have just brought
-// them into L2), one chunk ahead, so ring C never waits for this wave.  After
+// them into L2), two chunks ahead in two register sets used in turn, so ring
+// C never waits for this wave.  After
 // the last chunk Sc goes to the lo slots for the chain.
 __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                               int lane) {
@@ -1289,17 +1298,15 @@ __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, 
     f32x4 Sc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) Sc[t] = zero4();
-    u32x4 kc[16], kn[16];
     auto load_kt = [&](int c, u32x4 (&k)[16]) {
         const int cc = min(c, x.nch - 1);
         const u32x4* src = a.ws.KT + ((size_t)(x.chunk0 + cc) * a.HK + x.hk) * (16 * 64) + lane;
 #pragma unroll
         for (int f = 0; f < 16; ++f) k[f] = src[f * 64];
     };
-    load_kt(0, kc);
-    for (int c = 0; c < x.nch; ++c) {
-        load_kt(c + 1, kn);
-        if (!w.until([&] { return lds_ld(&sm.dvready) >= c + 1; })) return;
+    // one chunk with K^T in kc; then chunk c + 2's K^T goes into kc
+    auto step = [&](int c, u32x4 (&kc)[16]) -> bool {
+        if (!w.until([&] { return lds_ld(&sm.dvready) >= c + 1; })) return false;
         asm volatile("" ::: "memory");
         const LoHand& lh = sm.lo[c % kLoSlots];
         f32x4 d[4];
@@ -1333,8 +1340,16 @@ __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, 
             for (int t = 0; t < 8; ++t)
                 Sc[t] = mfma16_bf16(__builtin_bit_cast(bf16x8, kc[t * 2 + kb]), lo[kb], Sc[t]);
         }
-#pragma unroll
-        for (int f = 0; f < 16; ++f) kc[f] = kn[f];
+        load_kt(c + 2, kc);
+        return true;
+    };
+    u32x4 k0[16], k1[16];
+    load_kt(0, k0);
+    load_kt(1, k1);
+    // step() is false only when a bounded wait gave up
+    for (int c = 0; c < x.nch; c += 2) {
+        if (!step(c, k0)) return;
+        if (c + 1 < x.nch && !step(c + 1, k1)) return;
     }
     // every chunk's slot has been read: Sc goes to the lo slots
     f32x4* dst = &sm.lo[0].d[0][0];
