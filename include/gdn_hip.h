@@ -47,7 +47,7 @@ size_t deltanet_prefill_workspace_size(int B, int T, int HV, int DK, int DV, int
  * code under HIP graph capture, tight serving loops.  Every call on one GPU
  * shares that array, so calls that overlap on one GPU (two streams, say)
  * race; calls in one stream do not.  A call whose live workspace exceeds the
- * array (more than 733 chunk-heads, e.g. T > 1408 at HV = 32) returns
+ * array (more than 712 chunk-heads, e.g. T > 1408 at HV = 32) returns
  * hipErrorInvalidValue before any launch. */
 hipError_t deltanet_chunk_prefill_noalloc(const void* q, const void* k, const void* v,
                                           const float* g, const float* beta, void* o,
@@ -57,7 +57,7 @@ hipError_t deltanet_chunk_prefill_noalloc(const void* q, const void* k, const vo
 
 /* Workspace bytes for dump_debug = 0 only (no counterpart in the reference,
  * whose size always includes its debug regions): a 256-byte header with the
- * status word, then 12 KB per (chunk, v-head). */
+ * status word, then 69 KB per (chunk, v-head). */
 size_t deltanet_prefill_live_workspace_size(int B, int T, int HV, int DK, int DV,
                                             int chunk_size);
 
@@ -121,6 +121,25 @@ hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k, const void
                                         const void* dt_bias, void* o, float* state, int B, int T,
                                         int HV, int HQK, int io_dtype, void* workspace,
                                         size_t workspace_bytes, hipStream_t stream);
+
+/* Prefill with the gated RMSNorm fused into its output stage (the reference
+ * runs that post-op as a separate TensorRT plugin, kernel::gatedRmsNormForward,
+ * export/patches/orin_text_engine/files/cpp/kernels/gatedRmsNorm/gatedRmsNormKernel.h:17-18,
+ * after the prefill).  Same arguments as deltanet_chunk_prefill (dump_debug = 0)
+ * plus z (bf16 [B, T, HV, 128]), norm_weight (bf16 [128]) and eps; y (bf16
+ * [B, T, HV, 128]) receives gated_rmsnorm(o, z) = bf16(bf16(w * bf16(o *
+ * rsqrt(mean(o^2) + eps))) * silu(z)), o being the bf16 output of
+ * deltanet_chunk_prefill, and o itself is never stored.  The fused path runs
+ * when the whole scan grid (8 * B * HV work-groups, rounded up) is resident
+ * at once; otherwise the prefill writes o into y and the gated RMSNorm rewrites
+ * it in place.  Workspace as for deltanet_chunk_prefill. */
+hipError_t deltanet_chunk_prefill_norm(const void* q, const void* k, const void* v,
+                                       const float* g, const float* beta, const void* z,
+                                       const void* norm_weight, float eps, void* y,
+                                       const float* initial_state, float* final_state, int B,
+                                       int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                                       void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream);
 
 /* Variable-length prefill (no counterpart in the reference kernel: its torch
  * fallback drops cu_seqlens, transformers modeling_qwen3_5.py:259).

@@ -54,6 +54,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 namespace gdn {
@@ -77,6 +78,9 @@ __host__ __device__ constexpr int tri_base(int mt) { return mt < 3 ? mt : 4; }
 //   Q         Q rows as fp16 fragments, per (chunk, k-head)          16 KB
 //   KT        K^T as bf16 A-operand fragments of the state update, per
 //             (chunk, k-head): tile t = dk block, k-block kb = tokens        16 KB
+//   SSQ       gated-RMSNorm epilogue: per (slice, token) the slice's sum of
+//             squares of o, fp32 bits with the sign bit clear once written
+//             (the prep fills the slots with all-ones)                        2 KB
 // A 256-byte header in front holds the status word.
 constexpr size_t kFrag = 64 * 16;                      // one fragment: 1 KB
 constexpr size_t kTriBytes = (size_t)kTri * kFrag;     // 6 KB
@@ -84,6 +88,7 @@ constexpr size_t kWBytes = 16 * kFrag;                 // 16 KB
 constexpr size_t kGateBytes = 1024;
 constexpr size_t kQBytes = 16 * kFrag;                 // 16 KB
 constexpr size_t kKTBytes = 16 * kFrag;                // 16 KB
+constexpr size_t kSsqBytes = (size_t)kSlices * kChunk * 4;   // 2 KB
 constexpr size_t kHeaderBytes = 256;
 
 // gates record: float offsets
@@ -97,6 +102,7 @@ struct Workspace {
     float* gates;       // [chunk-head][256]
     half8* Q;           // Q fragments [chunk * HK + hk][mt * 4 + kb][64]
     u32x4* KT;          // K^T bf16 fragments [chunk * HK + hk][t * 2 + kb][64]
+    uint32_t* ssq;      // [chunk-head][slice][64] fp32 bits, sign bit set = not yet written
     unsigned* status;   // bit 0: a bounded wait gave up
     float* dbgT;        // optional [chunk-head][64][64]: T = (I - A)^-1
     float* dbgA;        // optional: A
@@ -111,7 +117,7 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 // Byte layout of the workspace for `nch` chunk-heads.  The debug regions stay
 // last: the torch binding finds them from the end.
 struct WsLayout {
-    size_t ti, tilo, m, w, gates, q, kt, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
+    size_t ti, tilo, m, w, gates, q, kt, ssq, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
     __host__ explicit WsLayout(size_t nch) {
         size_t off = kHeaderBytes;
         ti = off;    off += align256(nch * kTriBytes);
@@ -121,6 +127,7 @@ struct WsLayout {
         gates = off; off += align256(nch * kGateBytes);
         q = off;     off += align256(nch * kQBytes);
         kt = off;    off += align256(nch * kKTBytes);
+        ssq = off;   off += align256(nch * kSsqBytes);
         live = off;
         dbgT = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgA = off;  off += align256(nch * kChunk * kChunk * 4);
@@ -413,6 +420,10 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         return;
     (void)seq;
     const size_t ch = (size_t)cid * HV + hv;
+    // this call's gated-RMSNorm slots start invalid (2 KB: 16 bytes a thread)
+    if (tid < kSlices * kChunk / 4)
+        reinterpret_cast<u32x4*>(ws.ssq + ch * (kSlices * kChunk))[tid] =
+            u32x4{~0u, ~0u, ~0u, ~0u};
 
     // ---- global loads, all issued before any is consumed.  Rows past the
     // chunk's end read the last valid row and are zeroed afterwards.
@@ -859,6 +870,14 @@ struct ScanSmem {
     int abort;       // a bounded wait ran out: every wave stops
     int seqsel;
     int red[kScanWaves];
+    // norm epilogue, per output wave: a chunk's sums of squares per (tile,
+    // token, lane group), then per token the sum over the 8 slices
+    float npart[2][4][16][4];
+    float ntot[2][64];
+    int npub[2];     // per output wave: chunks whose partial sums are in npart
+    int nfree[2];    // per output wave: chunks whose npart the norm wave has read
+    int ntok[2];     // per output wave: chunks whose row totals are in ntot
+    int nread[2];    // per output wave: chunks whose ntot it has read
 };
 
 __device__ __forceinline__ int lds_ld(const int* p) {
@@ -908,7 +927,10 @@ struct Waiter {
 struct ScanArgs {
     PrepIn in;
     Workspace ws;
-    uint16_t* o;
+    uint16_t* o;              // o, or y = gated_rmsnorm(o, z) for the norm epilogue
+    const uint16_t* z;        // norm epilogue: gate input z, [token][HV][128] bf16
+    const uint16_t* nw;       // norm epilogue: weight [128] bf16
+    float eps;
     const float* s0;
     float* sf;
     const int32_t* cu;
@@ -1359,11 +1381,149 @@ __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, 
     if (lane == 0) lds_st(&sm.scdone, 1);
 }
 
+// Gated-RMSNorm epilogue (kNorm; bf16 o, z and weight), y = gated_rmsnorm(o, z)
+// with the transformers rounding steps (modeling_qwen3_5.py:175-184):
+// n = bf16(o * rsqrt(mean(o^2) + eps)), h = bf16(w * n), y = bf16(h * silu(z)),
+// o being the bf16 value the plain prefill would store.  A row's 128 columns
+// are spread over the 8 slice groups of its head, so each group publishes its
+// 16-column sum of squares per token in a 32-bit slot (device-scope atomic
+// store of the fp32 bits, sign bit clear; the prep fills every slot with
+// all-ones first, and each slot is written once per call, so a reader needs
+// no ordering between slots) and sums the 8 slots in slice order, the same
+// sum in every group.  A chunk is finished one chunk of the wave later, when
+// the other groups' slots are normally in.
+__device__ inline uint32_t* ssq_slots(const ScanArgs& a, const ScanCtx& x, int c) {
+    return a.ws.ssq + ((size_t)(x.chunk0 + c) * a.HV + x.hv) * (kSlices * kChunk);
+}
+
+// Norm wave (wave 4, norm epilogue only): the device-scope traffic of the
+// row sums, kept off the output waves, whose loads would otherwise wait behind
+// each device-scope store.  Per chunk c, in order: token L's sum over this
+// slice's 16 columns (lane groups in order) from npart into its slot; then
+// chunk c - 1's 8 slots of each token, polled until valid and summed in
+// slice order, into ntot for the output wave of c - 1.
+__device__ void run_norm(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                         int lane) {
+    auto totals = [&](int cg) -> bool {
+        const int jg = cg & 1, kg = cg >> 1;
+        const uint32_t* slots = ssq_slots(a, x, cg);
+        uint32_t v[kSlices];
+        auto poll = [&] {
+            bool ok = true;
+#pragma unroll
+            for (int sl = 0; sl < kSlices; ++sl) {
+                v[sl] = __hip_atomic_load(slots + sl * kChunk + lane, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+                ok = ok && (v[sl] >> 31) == 0;
+            }
+            return __all(ok) != 0;
+        };
+        if (!w.until(poll)) return false;
+        float tot = 0.f;
+#pragma unroll
+        for (int sl = 0; sl < kSlices; ++sl) tot += __uint_as_float(v[sl]);
+        // ntot[jg] held chunk cg - 2's totals until its output wave read them
+        if (!w.until([&] { return lds_ld(&sm.nread[jg]) >= kg; })) return false;
+        asm volatile("" ::: "memory");
+        sm.ntot[jg][lane] = tot;
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.ntok[jg], kg + 1);
+        return true;
+    };
+    for (int c = 0; c < x.nch; ++c) {
+        const int jc = c & 1, kc = c >> 1;
+        if (!w.until([&] { return lds_ld(&sm.npub[jc]) >= kc + 1; })) return;
+        asm volatile("" ::: "memory");
+        const f32x4 pp = *reinterpret_cast<const f32x4*>(&sm.npart[jc][lane >> 4][lane & 15][0]);
+        const float ssl = ((pp[0] + pp[1]) + pp[2]) + pp[3];
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.nfree[jc], kc + 1);
+        __hip_atomic_store(ssq_slots(a, x, c) + x.sl * kChunk + lane,
+                           __float_as_uint(ssl) & 0x7fffffffu, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (c > 0 && !totals(c - 1)) return;
+    }
+    if (x.nch > 0) (void)totals(x.nch - 1);
+}
+
 // Output wave j (0 or 1): chunks j, j + 2, ...
-template <int kRaw>
+template <int kRaw, bool kNorm>
 __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                            int j, int lane) {
     const int lg = lane >> 4, lm = lane & 15;
+    // norm epilogue: this lane's weights (columns 4 lg .. + 3 of the slice)
+    // and the wave's previous chunk, held until it is finished
+    float wn[4] = {0.f, 0.f, 0.f, 0.f};
+    uint2 xprev[4];
+    int cprev = -1;
+    if constexpr (kNorm) {
+        const uint2 wr = *reinterpret_cast<const uint2*>(a.nw + kSliceCols * x.sl + 4 * lg);
+        wn[0] = bf16_bits_to_f32(wr.x & 0xffffu);
+        wn[1] = bf16_bits_to_f32(wr.x >> 16);
+        wn[2] = bf16_bits_to_f32(wr.y & 0xffffu);
+        wn[3] = bf16_bits_to_f32(wr.y >> 16);
+    }
+    // y for chunk cf from its o values xo: gather() issues the loads of cf's
+    // z, so they land while the wave waits for and computes its next chunk;
+    // finish() takes the rows' sums of squares over all 128 columns from the
+    // norm wave (through ntot) and stores y.
+    struct Gather {
+        uint2 z[4];
+    };
+    auto gather = [&](int cf, Gather& gt) {
+        const int rows = min(kChunk, x.len - cf * kChunk);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int r = min(16 * mt + lm, rows - 1);
+            gt.z[mt] = *reinterpret_cast<const uint2*>(
+                a.z + ((size_t)(x.tok_base + cf * kChunk + r) * a.HV + x.hv) * kDV +
+                kSliceCols * x.sl + 4 * lg);
+        }
+    };
+    auto finish = [&](int cf, const uint2 (&xo)[4], Gather& gt) -> bool {
+        const int rows = min(kChunk, x.len - cf * kChunk);
+        const int kf = cf >> 1;
+        if (!w.until([&] { return lds_ld(&sm.ntok[j]) >= kf + 1; })) return false;
+        asm volatile("" ::: "memory");
+        float tsum[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) tsum[mt] = sm.ntot[j][16 * mt + lm];
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.nread[j], kf + 1);
+
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const float ss = tsum[mt];
+            const float rs = 1.0f / sqrtf(ss / (float)kDV + a.eps);
+            const uint32_t xw[2] = {xo[mt].x, xo[mt].y};
+            const uint32_t zw[2] = {gt.z[mt].x, gt.z[mt].y};
+            uint32_t out[2];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float xv = bf16_bits_to_f32(h ? xw[p] >> 16 : xw[p] & 0xffffu);
+                    const float zv = bf16_bits_to_f32(h ? zw[p] >> 16 : zw[p] & 0xffffu);
+                    const float n = bf16_bits_to_f32(f32_to_bf16_bits(xv * rs));
+                    const float hv = bf16_bits_to_f32(f32_to_bf16_bits(wn[2 * p + h] * n));
+                    const float sz = zv * __builtin_amdgcn_rcpf(
+                                              1.0f + __builtin_amdgcn_exp2f(zv * -1.44269504088896341f));
+                    pk |= (uint32_t)f32_to_bf16_bits(hv * sz) << (16 * h);
+                }
+                out[p] = pk;
+            }
+            const int r = 16 * mt + lm;
+            if (r < rows) {
+                uint2* dst = reinterpret_cast<uint2*>(
+                    a.o + ((size_t)(x.tok_base + cf * kChunk + r) * a.HV + x.hv) * kDV +
+                    kSliceCols * x.sl + 4 * lg);
+                *dst = make_uint2(out[0], out[1]);
+            }
+        }
+        return true;
+    };
+    Gather gt;
     // Q and M fragments and s e^c go straight to registers; the next chunk's
     // loads are issued as soon as the current chunk's products have read them
     half8 qf[16], mf[kTri];
@@ -1385,6 +1545,9 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
     load(j);
     for (int c = j; c < x.nch; c += 2) {
         const int hs = c % kHand;
+        if constexpr (kNorm) {
+            if (cprev >= 0) gather(cprev, gt);
+        }
         if (!w.until([&] { return lds_ld(&sm.ready) >= c + 1; })) return;
         asm volatile("" ::: "memory");
         half8 hsf[4], hvf[2];
@@ -1414,6 +1577,7 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
         asm volatile("" : "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));
         load(c + 2);
         const int rows = min(kChunk, x.len - c * kChunk);
+        uint2 xnew[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const int r = 16 * mt + lm;
@@ -1426,12 +1590,41 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
             }
             pk.x = b[0] | (b[1] << 16);
             pk.y = b[2] | (b[3] << 16);
-            if (r < rows) {
+            if constexpr (kNorm) {
+                // this lane's 4 columns of token r: sum of squares of the
+                // bf16 values, to LDS for the per-token sum below
+                float ssp = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xv = bf16_bits_to_f32(b[e]);
+                    ssp = fmaf(xv, xv, ssp);
+                }
+                if (mt == 0 && !w.until([&] { return lds_ld(&sm.nfree[j]) >= (c >> 1); }))
+                    return;
+                sm.npart[j][mt][lm][lg] = ssp;
+                xnew[mt] = pk;
+            } else if (r < rows) {
                 uint2* dst = reinterpret_cast<uint2*>(
                     a.o + ((size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv) * kDV +
                     kSliceCols * x.sl + 4 * lg);
                 *dst = pk;
             }
+        }
+        if constexpr (kNorm) {
+            // this chunk's partial sums to the norm wave
+            lds_wait_all();
+            if (lane == 0) lds_st(&sm.npub[j], (c >> 1) + 1);
+            // the wave's previous chunk: the other groups' sums are in by now
+            if (cprev >= 0 && !finish(cprev, xprev, gt)) return;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) xprev[mt] = xnew[mt];
+            cprev = c;
+        }
+    }
+    if constexpr (kNorm) {
+        if (cprev >= 0) {
+            gather(cprev, gt);
+            (void)finish(cprev, xprev, gt);
         }
     }
 }
@@ -1439,7 +1632,7 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
 // s0 and sf may be the same buffer: the chain reads its elements of the
 // initial state before its first chunk and writes the same elements after its
 // last, and no other wave touches either.
-template <int kRaw, bool kDbg>
+template <int kRaw, bool kDbg, bool kNorm = false>
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     __shared__ ScanSmem sm;
     const int tid = threadIdx.x;
@@ -1487,20 +1680,32 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
         lds_st(&sm.dvready, 0);
         lds_st(&sm.lodone, 0);
         lds_st(&sm.scdone, 0);
+        lds_st(&sm.npub[0], 0);
+        lds_st(&sm.npub[1], 0);
+        lds_st(&sm.nfree[0], 0);
+        lds_st(&sm.nfree[1], 0);
+        lds_st(&sm.ntok[0], 0);
+        lds_st(&sm.ntok[1], 0);
+        lds_st(&sm.nread[0], 0);
+        lds_st(&sm.nread[1], 0);
         lds_st(&sm.abort, 0);
     }
     __syncthreads();
     const Waiter w{&sm.abort, a.ws.status, a.spin};
     // Waves go to SIMDs round-robin (wave w on SIMD w % 4): the chain has
-    // SIMD 0 to itself (wave 4 exits at once); the loaders share SIMDs 1 and 2
+    // SIMD 0 to itself but for the norm wave (norm epilogue only; otherwise
+    // wave 4 exits at once), which issues a few memory operations per chunk;
+    // the loaders share SIMDs 1 and 2
     // with the producer and an output wave, the lo helper SIMD 3 with the
     // other output wave.
     switch (wave) {
         case 0: run_chain<kDbg>(sm, a, w, x, lane); break;
         case 1: run_producer<kRaw>(sm, a, w, x, lane); break;
-        case 2: run_output<kRaw>(sm, a, w, x, 0, lane); break;
-        case 3: run_output<kRaw>(sm, a, w, x, 1, lane); break;
-        case 4: break;
+        case 2: run_output<kRaw, kNorm>(sm, a, w, x, 0, lane); break;
+        case 3: run_output<kRaw, kNorm>(sm, a, w, x, 1, lane); break;
+        case 4:
+            if constexpr (kNorm) run_norm(sm, a, w, x, lane);
+            break;
         case 5: run_loader(sm, a, w, x, 1, lane); break;
         case 6: run_loader(sm, a, w, x, 0, lane); break;
         default:
@@ -1512,11 +1717,20 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
 
 // raw: 0 for prepared inputs, 1 / 2 for raw bf16 / fp16 q, k (normalised in
 // the prep; then v and o have that dtype too).
+// The gated-RMSNorm epilogue's inputs (bf16 z [token][HV][128], bf16 weight
+// [128], eps); o then receives y.
+struct NormIn {
+    const uint16_t* z;
+    const uint16_t* w;
+    float eps;
+};
+
 hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
                           hipStream_t stream, int dump_debug, hipEvent_t* ev = nullptr,
-                          int only = -1, unsigned spin = kDefaultSpin) {
+                          int only = -1, unsigned spin = kDefaultSpin,
+                          const NormIn* norm = nullptr) {
     const WsLayout L(nch_bound * (size_t)HV);
     const size_t need = dump_debug ? L.total : L.live;
     if (workspace_bytes < need) return hipErrorInvalidValue;
@@ -1529,6 +1743,7 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     ws.gates = reinterpret_cast<float*>(base + L.gates);
     ws.Q = reinterpret_cast<half8*>(base + L.q);
     ws.KT = reinterpret_cast<u32x4*>(base + L.kt);
+    ws.ssq = reinterpret_cast<uint32_t*>(base + L.ssq);
     ws.status = reinterpret_cast<unsigned*>(base);
     if (dump_debug) {
         ws.dbgT = reinterpret_cast<float*>(base + L.dbgT);
@@ -1570,9 +1785,15 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     sa.HK = HK;
     sa.nch_bound = (int)nch_bound;
     sa.spin = spin;
+    if (norm) {
+        sa.z = norm->z;
+        sa.nw = norm->w;
+        sa.eps = norm->eps;
+    }
     const int pairs = N * HV;
     const int grp = (pairs + 7) / 8;
-    auto scan = raw == 1 ? gdn_scan_kernel<1, false>
+    auto scan = norm ? gdn_scan_kernel<0, false, true>
+                : raw == 1 ? gdn_scan_kernel<1, false>
                 : raw == 2 ? gdn_scan_kernel<2, false>
                 : dump_debug ? gdn_scan_kernel<0, true> : gdn_scan_kernel<0, false>;
     hipLaunchKernelGGL(scan, dim3((unsigned)(grp * 8 * kSlicesPerHead)), dim3(kScanThreads), 0,
@@ -1633,6 +1854,55 @@ extern "C" hipError_t deltanet_chunk_prefill(const void* q, const void* k, const
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
     return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
                           T, B * T, HV, HQK, nc, workspace, workspace_bytes, stream, dump_debug);
+}
+
+namespace {
+// Compute units of the current device, queried once per device.
+int device_cus() {
+    constexpr int kDevs = 64;
+    static std::atomic<int> cache[kDevs];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+}  // namespace
+
+extern "C" hipError_t deltanet_chunk_prefill_norm(const void* q, const void* k, const void* v,
+                                                  const float* g, const float* beta, const void* z,
+                                                  const void* norm_weight, float eps, void* y,
+                                                  const float* initial_state, float* final_state,
+                                                  int B, int T, int HV, int HQK, int DK, int DV,
+                                                  int chunk_size, void* workspace,
+                                                  size_t workspace_bytes, hipStream_t stream) {
+    if (!dims_ok(HV, HQK, DK, DV, chunk_size) || B <= 0 || T < 0) return hipErrorInvalidValue;
+    if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !z || !norm_weight || !y))
+        return hipErrorInvalidValue;
+    if (!(eps >= 0.f)) return hipErrorInvalidValue;
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    // The epilogue's groups wait on each other (the 8 slice groups of a head
+    // share every row's sum of squares), so it runs only when the whole scan
+    // grid is resident at once; otherwise the prefill writes o into y and the
+    // gated RMSNorm kernel rewrites it in place.
+    const long long groups = (long long)((B * HV + 7) / 8) * 8 * kSlicesPerHead;
+    const int cus = device_cus();
+    const NormIn n{static_cast<const uint16_t*>(z), static_cast<const uint16_t*>(norm_weight), eps};
+    if (cus > 0 && groups <= cus)
+        return launch_prefill(plain_in(q, k, v, g, beta), 0, y, initial_state, final_state,
+                              nullptr, B, T, B * T, HV, HQK, nc, workspace, workspace_bytes,
+                              stream, 0, nullptr, -1, kDefaultSpin, &n);
+    hipError_t e = launch_prefill(plain_in(q, k, v, g, beta), 0, y, initial_state, final_state,
+                                  nullptr, B, T, B * T, HV, HQK, nc, workspace, workspace_bytes,
+                                  stream, 0);
+    if (e != hipSuccess || T == 0) return e;
+    return gdn_gated_rmsnorm_forward(y, z, norm_weight, y, (int64_t)B * T * HV, kDV, eps,
+                                     GDN_DTYPE_BF16, GDN_DTYPE_BF16, stream);
 }
 
 extern "C" hipError_t deltanet_prefill_status(const void* workspace, size_t workspace_bytes,
@@ -1826,7 +2096,7 @@ extern "C" hipError_t deltanet_chunk_prefill_l2norm(
 // Allocation-free prefill: the workspace is a file-scope device array.
 // ---------------------------------------------------------------------------
 // 48 MiB per GPU that loads the library, held until the process ends: the
-// live workspace of up to (48 MiB - 256 B) / 67 KB = 733 chunk-heads, e.g.
+// live workspace of up to (48 MiB - 256 B) / 69 KB = 712 chunk-heads, e.g.
 // T <= 1408 at HV = 32 (22 chunks).
 constexpr size_t kNoAllocScratchBytes = size_t(48) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];

@@ -9,7 +9,8 @@
 // libgdn_hip.so (include/gdn_hip.h) with raw pointers; no torch types cross
 // that boundary.  New relative to the reference: a trailing keyword
 // `cu_seqlens` (varlen prefill), `recurrent_step` (decode),
-// `gated_rmsnorm`, `chunk_prefill_fused` (the TensorRT adapter's whole GDN
+// `gated_rmsnorm`, `chunk_prefill_norm` (prefill with the gated RMSNorm in its
+// output stage), `chunk_prefill_fused` (the TensorRT adapter's whole GDN
 // step on raw inputs) and the causal conv1d ops `causal_conv1d_fwd` /
 // `causal_conv1d_update` that produce q/k/v upstream of the recurrence.
 #include <torch/extension.h>
@@ -196,6 +197,71 @@ std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tens
                                             std::optional<at::Tensor> s0,
                                             std::optional<at::Tensor> cu_seqlens) {
     return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/true);
+}
+
+// Prefill with the gated RMSNorm fused into its output stage: returns
+// [y, final_state], y = gated_rmsnorm(o, z, weight, eps) for the o that
+// chunk_prefill would return (bf16 o, z and weight).
+std::vector<at::Tensor> chunk_prefill_norm(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
+                                           at::Tensor beta, at::Tensor z, at::Tensor weight,
+                                           std::optional<at::Tensor> s0, double eps,
+                                           bool checked) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda() &&
+                    z.is_cuda() && weight.is_cuda(),
+                "all inputs must be CUDA tensors");
+    TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
+                    v.scalar_type() == at::kBFloat16 && z.scalar_type() == at::kBFloat16 &&
+                    weight.scalar_type() == at::kBFloat16,
+                "q/k/v/z/weight must be bf16");
+    TORCH_CHECK(g.scalar_type() == at::kFloat && beta.scalar_type() == at::kFloat,
+                "g/beta must be fp32");
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && g.dim() == 3 && beta.dim() == 3,
+                "bad ranks");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto qc = q.contiguous();
+    auto kc = k.contiguous();
+    auto vc = v.contiguous();
+    auto gc = g.contiguous();
+    auto bc = beta.contiguous();
+    auto zc = z.contiguous();
+    auto wc = weight.contiguous();
+    const int64_t B = qc.size(0), T = qc.size(1), HQK = qc.size(2), DK = qc.size(3);
+    const int64_t HV = vc.size(2), DV = vc.size(3);
+    TORCH_CHECK(kc.sizes() == qc.sizes(), "q/k shape mismatch");
+    TORCH_CHECK(vc.size(0) == B && vc.size(1) == T && gc.size(0) == B && gc.size(1) == T &&
+                    gc.size(2) == HV && bc.sizes() == gc.sizes(),
+                "batch/time/head mismatch");
+    TORCH_CHECK(zc.sizes() == vc.sizes(), "z must have v's shape [B, T, HV, 128]");
+    TORCH_CHECK(wc.dim() == 1 && wc.size(0) == DV, "weight must be [128]");
+    TORCH_CHECK(HV % HQK == 0, "HV must be a multiple of HQK");
+    TORCH_CHECK(DK == 128 && DV == 128, "only DK = DV = 128 is supported");
+    auto y = at::empty_like(vc);
+    auto sf = at::empty({B, HV, DK, DV}, vc.options().dtype(at::kFloat));
+    const float* s0p = nullptr;
+    at::Tensor s0c;
+    if (s0.has_value()) {
+        TORCH_CHECK(s0->is_cuda(), "s0 must be a CUDA tensor");
+        s0c = s0->to(at::kFloat).contiguous();
+        TORCH_CHECK(s0c.dim() == 4 && s0c.size(0) == B && s0c.size(1) == HV &&
+                        s0c.size(2) == DK && s0c.size(3) == DV,
+                    "s0 must be [B, HV, DK, DV]");
+        s0p = s0c.data_ptr<float>();
+    }
+    const size_t ws_bytes = deltanet_prefill_live_workspace_size((int)B, (int)T, (int)HV, (int)DK,
+                                                                 (int)DV, kChunk);
+    TORCH_CHECK(ws_bytes > 0, "unsupported prefill configuration");
+    auto ws = at::empty({(int64_t)ws_bytes}, vc.options().dtype(at::kByte));
+    check_hip(deltanet_chunk_prefill_norm(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                          gc.data_ptr<float>(), bc.data_ptr<float>(),
+                                          zc.data_ptr(), wc.data_ptr(), (float)eps, y.data_ptr(),
+                                          s0p, sf.data_ptr<float>(), (int)B, (int)T, (int)HV,
+                                          (int)HQK, (int)DK, (int)DV, kChunk, ws.data_ptr(),
+                                          ws_bytes, current_stream()),
+              "deltanet_chunk_prefill_norm");
+    if (checked)
+        check_hip(deltanet_prefill_status(ws.data_ptr(), ws_bytes, current_stream()),
+                  "deltanet_chunk_prefill_norm (status word)");
+    return {y, sf};
 }
 
 at::Tensor recurrent_step(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
@@ -407,6 +473,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "diagonal-block inversion, M, and the state at each chunk's start",
           "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
           "cu_seqlens"_a = std::nullopt);
+    m.def("chunk_prefill_norm", &chunk_prefill_norm,
+          "prefill with the gated RMSNorm fused into its output stage; returns [y, final_state], "
+          "y = gated_rmsnorm(o, z, weight, eps) for chunk_prefill's o",
+          "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "z"_a, "weight"_a, "s0"_a = std::nullopt,
+          pybind11::kw_only(), "eps"_a = 1e-6, "checked"_a = false);
     m.def("_chunk_prefill_spin_limit", &chunk_prefill_spin_limit,
           "test entry: prefill with the scan's bounded waits limited to `spin` polls; returns "
           "[o, final_state, status]",

@@ -13,6 +13,8 @@ The compiled pieces live next to this file:
   chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
   recurrent_step(q, k, v, g, beta, state, *, qk_l2norm=False) -> o
                                                         (state updated in place)
+  chunk_prefill_norm(q, k, v, g, beta, z, weight, s0=None, *, eps=1e-6, checked=False)
+                          -> [gated_rmsnorm(o, z, weight), final_state]
   chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state) -> o
                           raw q/k/v and gate inputs     (state updated in place)
   gated_rmsnorm(x, z, weight, eps=1e-6) -> y
@@ -59,6 +61,10 @@ def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False
 
 def chunk_prefill_debug(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
     return load().chunk_prefill_debug(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens)
+
+
+def chunk_prefill_norm(q, k, v, g, beta, z, weight, s0=None, eps=1e-6):
+    return load().chunk_prefill_norm(q, k, v, g, beta, z, weight, s0, eps=eps)
 
 
 def chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state):

@@ -33,6 +33,8 @@ _PROTOS = {
     "deltanet_tcop_chunk_prefill": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 7 +
                                     [vp, c_size_t, hipStream_t, c_int]),
     "deltanet_prefill_live_workspace_size": (c_size_t, [c_int] * 6),
+    "deltanet_chunk_prefill_norm": (hipError_t, [vp, vp, vp, fp, fp, vp, vp, c_float, vp, fp, fp] +
+                                    [c_int] * 7 + [vp, c_size_t, hipStream_t]),
     "deltanet_chunk_prefill_noalloc": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] +
                                        [c_int] * 7 + [hipStream_t]),
     "deltanet_prefill_varlen_workspace_size": (c_size_t, [c_int] * 6),

@@ -45,7 +45,7 @@ def test_noalloc_matches_workspace_entry(dev):
 
 def test_noalloc_rejects_oversize(dev):
     lib = capi.lib()
-    # 23 chunks x 32 heads = 736 chunk-heads > 733
+    # 23 chunks x 32 heads = 736 chunk-heads > 712
     B, T, HK, HV, D = 1, 23 * 64, 16, 32, 128
     dummy = torch.empty(16, device=dev)
     p = dummy.data_ptr()
