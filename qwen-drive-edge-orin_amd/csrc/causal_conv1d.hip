@@ -20,6 +20,8 @@
 
 #include <math.h>
 
+#include <atomic>
+
 #include <algorithm>
 
 namespace gdn {
@@ -419,6 +421,23 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_update4_kernel(
     reinterpret_cast<u32x4*>(st)[1] = n1;
 }
 
+// Compute units of the current device, queried once per device (256 when
+// the query fails).
+int device_cus() {
+    constexpr int kDevs = 64;
+    static std::atomic<int> cache[kDevs];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            return 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 template <int IO, int WT, bool SILU, bool BIAS>
 hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, int B, int T, int D,
                       int K, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
@@ -426,10 +445,7 @@ hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, i
     const int n_ctiles = (D / 8 + kConvThreads - 1) / kConvThreads;
     // about two waves per SIMD (2 work-groups of 4 waves per CU), runs of
     // equal length up to kConvMaxRun tokens
-    int cus = 256, dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        cus = 256;
+    const int cus = device_cus();
     const int64_t per_row = (int64_t)B * n_ctiles;
     int64_t n_runs = (2LL * cus + per_row / 2) / per_row;
     n_runs = std::max<int64_t>(1, std::min<int64_t>(n_runs, T));

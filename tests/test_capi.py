@@ -220,3 +220,13 @@ def test_torch_extension_loads_and_checks_device():
     x = torch.zeros(1, 64, 8, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="CUDA"):
         ops.causal_conv1d_fwd(x, torch.zeros(64, 4, dtype=torch.bfloat16), None, True)
+
+
+def test_reference_module_names_import():
+    """The harness's module names (kernels/harness/parity_cuda.py:56,
+    kernels/parity_tco.py:28) import and expose its two ops."""
+    import importlib
+
+    for name in ("deltanet_chunk_cuda", "deltanet_chunk_cuda_tco"):
+        mod = importlib.import_module(name)
+        assert callable(mod.chunk_prefill) and callable(mod.chunk_prefill_debug), name
