@@ -9,7 +9,8 @@ resident in HBM before timing starts; successive steps rotate through enough
 input copies (> 256 MB) that the Infinity Cache cannot serve them, so the
 timed number is the cold one.  The warm (same inputs every step) number and
 the secondary workloads (gated RMSNorm, decode step, varlen prefill, causal
-conv1d prefill and decode update, the fused raw-input prefill) are
+conv1d prefill and decode update, the fused raw-input prefill, the prefill
+with the gated RMSNorm in its output stage) are
 reported in the same JSON line.
 
 Prints ONE JSON line.  `value` is TFLOP/s under the fixed dense FLOP
@@ -108,6 +109,30 @@ def bench_prefill(ops, dev, steps, warmup):
     algo_bytes = in_bytes + out_bytes
     return dict(cold_ms=cold_ms, warm_ms=warm_ms, flops=flops, algo_bytes=algo_bytes,
                 n_sets=len(sets), T=T, HV=HV)
+
+
+def bench_prefill_norm(ops, dev, steps, warmup):
+    """The prefill with the gated RMSNorm in its output stage (chunk_prefill_norm)
+    at T=1141 HV=32, cold inputs, against the two steps it replaces
+    (chunk_prefill, then gated_rmsnorm) on the same rotated inputs."""
+    import torch
+    import gdn_cases as gc
+
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    gen = torch.Generator().manual_seed(33)
+    z = torch.randn(*v.shape, generator=gen).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(v.shape[-1], generator=gen)).to(torch.bfloat16)
+    per = _bytes(q, k, v, g, beta, s0, z)
+    sets = rotation(lambda: (q, k, v, g, beta, s0, z, w), per, dev)
+    ms_f = time_calls(lambda i: ops.chunk_prefill_norm(*sets[i][:5], sets[i][6], sets[i][7],
+                                                       sets[i][5]), len(sets), steps, warmup)
+
+    def two(i):
+        o, _ = ops.chunk_prefill(*sets[i][:6])
+        ops.gated_rmsnorm(o, sets[i][6], sets[i][7], 1e-6)
+
+    ms_2 = time_calls(two, len(sets), steps, warmup)
+    return dict(ms_f=ms_f, ms_2=ms_2)
 
 
 def bench_varlen(ops, dev, steps, warmup):
@@ -407,7 +432,7 @@ def trace_from_profiles():
     if not p.exists():
         return {}
     out = {}
-    for m in re.finditer(r"^\| (gdn_prep_kernel<false,0>|gdn_scan_kernel<0,false>) \| \d+ \| "
+    for m in re.finditer(r"^\| (gdn_prep_kernel<false,0>|gdn_scan_kernel<0,false,false>) \| \d+ \| "
                          r"([0-9.]+) \|.*\| (\d+)x1 \| \d+ \|$", p.read_text(), flags=re.M):
         name = m.group(1).split("<")[0]
         grid = int(m.group(3))
@@ -607,6 +632,7 @@ def main():
         var = bench_varlen(ops, dev, max(10, args.steps // 10), 5)
         cv = bench_conv(ops, dev, args.steps, args.warmup)
         fu = bench_fused(ops, dev, args.steps, args.warmup)
+        pn = bench_prefill_norm(ops, dev, args.steps, args.warmup)
         hl = bench_hf_lane(ops, dev, args.steps, args.warmup)
         sp = bench_stream(dev, args.steps, args.warmup)
         line["secondary"] = {
@@ -632,6 +658,9 @@ def main():
                                                 "hbm_frac": round(cv["frac"], 4)},
             "fused_prefill_fp16_raw_T1141_HV32": {"us": round(fu["ms_f"] * 1e3, 2),
                                                   "adapter_chain_us": round(fu["ms_c"] * 1e3, 2)},
+            "prefill_gated_rmsnorm_fused_T1141_HV32": {
+                "us": round(pn["ms_f"] * 1e3, 2),
+                "us_prefill_then_gated_rmsnorm": round(pn["ms_2"] * 1e3, 2)},
             "hf_lane_chunk_gated_delta_rule_T1141_HV32": {
                 "us": round(hl["ms_k"] * 1e3, 2),
                 "us_torch_l2norm_eager": round(hl["ms_t"] * 1e3, 2)},
