@@ -341,6 +341,39 @@ __device__ bool locate_chunk(const int32_t* cu, int N, int T, int total, int cid
     return found;
 }
 
+// Store of a workspace record for the scan, at device scope (sc1): the line
+// is written through this XCD's L2 while the prep runs.  A plain store leaves
+// it dirty in L2, and the kernel's end must then write back every dirty line
+// before the next kernel may start (the eight XCDs' L2s are not coherent with
+// each other): after the prep's 30 MB of workspace that write-back held the
+// scan back ~5 us, with these stores ~1.3 us.  (Non-temporal stores avoid the
+// write-back too, but the lines then come back from HBM, which slows the
+// scan.)  The prep never waits for these stores.  The scan's o and state
+// stores stay plain: a wave's later loads complete only after its earlier
+// stores, and waiting behind write-through stores slowed the output waves by
+// more than the write-back they save.  A store of more than 8 bytes reads its data
+// registers after issue: a VALU write to them needs two wait states first,
+// which the compiler inserts after its own stores but cannot see inside an
+// asm statement, so the 16-byte form carries its own s_nop.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <typename V>
+__device__ __forceinline__ void st_through(V* p, const V& v) {
+    static_assert(sizeof(V) == 4 || sizeof(V) == 8 || sizeof(V) == 16, "4, 8 or 16 bytes");
+    if constexpr (sizeof(V) == 16) {
+        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p),
+                     "v"(__builtin_bit_cast(u32x4, v))
+                     : "memory");
+    } else if constexpr (sizeof(V) == 8) {
+        asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p),
+                     "v"(__builtin_bit_cast(u32x2, v))
+                     : "memory");
+    } else {
+        asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p),
+                     "v"(__builtin_bit_cast(uint32_t, v))
+                     : "memory");
+    }
+}
+
 // ---------------------------------------------------------------------------
 // prep kernel: one work-group (4 waves) per (chunk, v-head)
 // ---------------------------------------------------------------------------
@@ -422,8 +455,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     const size_t ch = (size_t)cid * HV + hv;
     // this call's gated-RMSNorm slots start invalid (2 KB: 16 bytes a thread)
     if (tid < kSlices * kChunk / 4)
-        reinterpret_cast<u32x4*>(ws.ssq + ch * (kSlices * kChunk))[tid] =
-            u32x4{~0u, ~0u, ~0u, ~0u};
+        st_through(reinterpret_cast<u32x4*>(ws.ssq + ch * (kSlices * kChunk)) + tid,
+                   u32x4{~0u, ~0u, ~0u, ~0u});
 
     // ---- global loads, all issued before any is consumed.  Rows past the
     // chunk's end read the last valid row and are zeroed afterwards.
@@ -527,7 +560,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         if (writer) {
             half8* qdst = ws.Q + ((size_t)cid * HK + hk) * 16 * 64;
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) qdst[(wave * 4 + kb) * 64 + lane] = qf[kb];
+            for (int kb = 0; kb < 4; ++kb) st_through(&qdst[(wave * 4 + kb) * 64 + lane], qf[kb]);
         }
     }
 
@@ -549,10 +582,10 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         sm.cl[lane] = cs * kLog2e;
         sm.b[lane] = bv;
         float* gr = ws.gates + ch * (kGateBytes / 4);
-        gr[kGBeta + lane] = bv;
-        gr[kGDec + lane] = lane < rows ? __builtin_amdgcn_exp2f((c63 - cs) * kLog2e) : 0.f;
-        gr[kGSec + lane] = scale * __builtin_amdgcn_exp2f(cs * kLog2e);
-        gr[kGC63 + lane] = lane == 0 ? c63 : 0.f;
+        st_through(&gr[kGBeta + lane], bv);
+        st_through(&gr[kGDec + lane], lane < rows ? __builtin_amdgcn_exp2f((c63 - cs) * kLog2e) : 0.f);
+        st_through(&gr[kGSec + lane], scale * __builtin_amdgcn_exp2f(cs * kLog2e));
+        st_through(&gr[kGC63 + lane], lane == 0 ? c63 : 0.f);
         if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
     }
     __syncthreads();
@@ -615,8 +648,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             mh[mt] = to_half4(val);
         }
         half8* mdst = ws.M + ch * (kTri * 64);
-        mdst[tri_base(wave) * 64 + lane] = cat8(mh[0], mh[1]);
-        if (wave >= 2) mdst[(tri_base(wave) + 1) * 64 + lane] = cat8(mh[2], mh[3]);
+        st_through(&mdst[tri_base(wave) * 64 + lane], cat8(mh[0], mh[1]));
+        if (wave >= 2) st_through(&mdst[(tri_base(wave) + 1) * 64 + lane], cat8(mh[2], mh[3]));
     }
     __syncthreads();
 
@@ -728,8 +761,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             }
             half8 hi, lo;
             split_hilo8(t0, t1, hi, lo);
-            tdst[(tri_base(mt) + kb) * 64 + lane] = hi;
-            ldst[(tri_base(mt) + kb) * 64 + lane] = lo;
+            st_through(&tdst[(tri_base(mt) + kb) * 64 + lane], hi);
+            st_through(&ldst[(tri_base(mt) + kb) * 64 + lane], lo);
         }
     }
 
@@ -756,7 +789,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                     bf16x8 kb16;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) kb16[e] = (__bf16)(float)kt[tt][kb][e];
-                    ktdst[((2 * wave + tt) * 2 + kb) * 64 + lane] = __builtin_bit_cast(u32x4, kb16);
+                    st_through(&ktdst[((2 * wave + tt) * 2 + kb) * 64 + lane],
+                               __builtin_bit_cast(u32x4, kb16));
                 }
             }
         }
@@ -786,7 +820,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                 acc0 = mfma16(kt[0][kb], bt, acc0);
                 acc1 = mfma16(kt[1][kb], bt, acc1);
             }
-            wdst[(mt * 4 + wave) * 64 + lane] = cat8(to_half4(-acc0), to_half4(-acc1));
+            st_through(&wdst[(mt * 4 + wave) * 64 + lane], cat8(to_half4(-acc0), to_half4(-acc1)));
         }
     }
 }
@@ -1014,10 +1048,27 @@ __device__ inline float v16_to_f32(uint32_t bits) {
 // straight from global memory three chunks ahead, in three register sets
 // used in turn (a set is refilled right after its chunk's products have read
 // it, so no copy ever waits for a load in flight).
+//
+// The producer also pulls V into L2 ahead of the loaders: V is the one scan
+// operand that comes from the caller's input rather than from what the prep
+// has just written, so it may still be in HBM, and ring P fetches it only one
+// chunk ahead.  Each step reads one dword of this slice's segment of every
+// row of chunk c + kVTouch (the L2 line holds the neighbouring slices'
+// segments, which their groups on the same XCD fetch themselves) into a
+// register that is only consumed three steps later, so the producer never
+// waits on it.
+constexpr int kVTouch = 6;
+
 template <int kRaw>
 __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                              int lane) {
     const int lg = lane >> 4, lm = lane & 15;
+    auto vtouch = [&](int cp) -> uint32_t {
+        const int c = min(cp, x.nch - 1);
+        const int r = min(lane, min(kChunk, x.len - c * kChunk) - 1);
+        const size_t row = (size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv;
+        return *reinterpret_cast<const uint32_t*>(a.in.v + row * kDV + kSliceCols * x.sl);
+    };
     auto load_t = [&](int c, half8 (&h)[kTri], half8 (&l)[kTri]) {
         const int cc = min(c, x.nch - 1);
         const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
@@ -1029,7 +1080,7 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
             l[f] = pl[f * 64];
         }
     };
-    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri]) -> bool {
+    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri], uint32_t& vt3) -> bool {
         // ring P of chunk c landed with loader group c - kLeadP (chunk 0's
         // lead with loader 0's first group)
         const int lc = max(c - kLeadP, 0);
@@ -1067,6 +1118,10 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
         }
         // the products have read this set: chunk c + 3's fragments go in
         load_t(c + 3, th, tl);
+        // the V touch of three steps ago has long landed: consume it, touch
+        // chunk c + kVTouch
+        asm volatile("" ::"v"(vt3));
+        vt3 = vtouch(c + kVTouch);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) st.U[mt][lane] = U[mt];
         lds_wait_all();
@@ -1078,11 +1133,12 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
     load_t(0, t0h, t0l);
     load_t(1, t1h, t1l);
     load_t(2, t2h, t2l);
+    uint32_t vt0 = vtouch(kVTouch - 3), vt1 = vtouch(kVTouch - 2), vt2 = vtouch(kVTouch - 1);
     // step() is false only when a bounded wait gave up
     for (int c = 0; c < x.nch; c += 3) {
-        if (!step(c, t0h, t0l)) return;
-        if (c + 1 < x.nch && !step(c + 1, t1h, t1l)) return;
-        if (c + 2 < x.nch && !step(c + 2, t2h, t2l)) return;
+        if (!step(c, t0h, t0l, vt0)) return;
+        if (c + 1 < x.nch && !step(c + 1, t1h, t1l, vt1)) return;
+        if (c + 2 < x.nch && !step(c + 2, t2h, t2l, vt2)) return;
     }
 }
 
