@@ -426,6 +426,12 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     PrepIn in, const int32_t* __restrict__ cu, int N, int T, int total, int HV, int HK,
     int nch_bound, float scale, Workspace ws) {
     __shared__ PrepSmem sm;
+    // The kernel arguments (232 bytes) span four 64-byte lines, which the
+    // scalar cache would otherwise fetch in three dependent round trips (each
+    // use waits before the branch that leads to the next): fields at most 32
+    // bytes apart, all requested together, cost one.
+    asm volatile("" ::"s"(in.q), "s"(in.A_log), "s"(cu), "s"(nch_bound), "s"(ws.TIlo),
+                 "s"(ws.gates), "s"(ws.ssq), "s"(ws.dbgT), "s"(ws.dbgM), "s"(ws.dbgS));
     const uint16_t* __restrict__ q = in.q;
     const uint16_t* __restrict__ k = in.k;
     const int tid = threadIdx.x;
@@ -1048,27 +1054,11 @@ __device__ inline float v16_to_f32(uint32_t bits) {
 // straight from global memory three chunks ahead, in three register sets
 // used in turn (a set is refilled right after its chunk's products have read
 // it, so no copy ever waits for a load in flight).
-//
-// The producer also pulls V into L2 ahead of the loaders: V is the one scan
-// operand that comes from the caller's input rather than from what the prep
-// has just written, so it may still be in HBM, and ring P fetches it only one
-// chunk ahead.  Each step reads one dword of this slice's segment of every
-// row of chunk c + kVTouch (the L2 line holds the neighbouring slices'
-// segments, which their groups on the same XCD fetch themselves) into a
-// register that is only consumed three steps later, so the producer never
-// waits on it.
-constexpr int kVTouch = 6;
 
 template <int kRaw>
 __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                              int lane) {
     const int lg = lane >> 4, lm = lane & 15;
-    auto vtouch = [&](int cp) -> uint32_t {
-        const int c = min(cp, x.nch - 1);
-        const int r = min(lane, min(kChunk, x.len - c * kChunk) - 1);
-        const size_t row = (size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv;
-        return *reinterpret_cast<const uint32_t*>(a.in.v + row * kDV + kSliceCols * x.sl);
-    };
     auto load_t = [&](int c, half8 (&h)[kTri], half8 (&l)[kTri]) {
         const int cc = min(c, x.nch - 1);
         const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
@@ -1080,7 +1070,7 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
             l[f] = pl[f * 64];
         }
     };
-    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri], uint32_t& vt3) -> bool {
+    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri]) -> bool {
         // ring P of chunk c landed with loader group c - kLeadP (chunk 0's
         // lead with loader 0's first group)
         const int lc = max(c - kLeadP, 0);
@@ -1118,10 +1108,6 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
         }
         // the products have read this set: chunk c + 3's fragments go in
         load_t(c + 3, th, tl);
-        // the V touch of three steps ago has long landed: consume it, touch
-        // chunk c + kVTouch
-        asm volatile("" ::"v"(vt3));
-        vt3 = vtouch(c + kVTouch);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) st.U[mt][lane] = U[mt];
         lds_wait_all();
@@ -1133,12 +1119,11 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
     load_t(0, t0h, t0l);
     load_t(1, t1h, t1l);
     load_t(2, t2h, t2l);
-    uint32_t vt0 = vtouch(kVTouch - 3), vt1 = vtouch(kVTouch - 2), vt2 = vtouch(kVTouch - 1);
     // step() is false only when a bounded wait gave up
     for (int c = 0; c < x.nch; c += 3) {
-        if (!step(c, t0h, t0l, vt0)) return;
-        if (c + 1 < x.nch && !step(c + 1, t1h, t1l, vt1)) return;
-        if (c + 2 < x.nch && !step(c + 2, t2h, t2l, vt2)) return;
+        if (!step(c, t0h, t0l)) return;
+        if (c + 1 < x.nch && !step(c + 1, t1h, t1l)) return;
+        if (c + 2 < x.nch && !step(c + 2, t2h, t2l)) return;
     }
 }
 
@@ -1691,6 +1676,12 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
 template <int kRaw, bool kDbg, bool kNorm = false>
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     __shared__ ScanSmem sm;
+    // The kernel arguments (280 bytes) span five 64-byte lines, which the
+    // scalar cache would otherwise fetch in three dependent round trips:
+    // fields at most 32 bytes apart, all requested together, cost one.
+    asm volatile("" ::"s"(a.in.q), "s"(a.in.beta), "s"(a.in.dt_bias), "s"(a.ws.M), "s"(a.ws.KT),
+                 "s"(a.ws.dbgT), "s"(a.ws.dbgC), "s"(a.z), "s"(a.s0), "s"(a.N), "s"(a.HK),
+                 "s"(a.spin));
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
 
