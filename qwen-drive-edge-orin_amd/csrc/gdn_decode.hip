@@ -11,10 +11,13 @@
 //   o = s (e^g b + delta (k . q))     (= s S_new^T q)
 //   S_new = e^g S + k delta^T         (written back in place)
 //
-// One work-group of 256 threads per (batch, v-head) holds the 128x128 fp32
-// state in registers: thread t owns columns 4*(t%32)..+3 of rows
-// (t/32) + 8m, m = 0..15, so every load/store instruction of a wave moves two
-// whole 512-byte rows.  Tokens t > 0 reuse the registers; HBM sees the
+// The state's columns evolve independently, so each (batch, v-head) is split
+// over two work-groups of 256 threads, one per half of the columns: thread t
+// of half h owns columns 64 h + 4 (t % 16) .. + 3 of rows (t / 16) + 16 m,
+// m = 0..7, so every load/store instruction of a wave moves four 256-byte
+// half rows.  Two groups of 32 state registers per thread (rather than one of
+// 64) leave room for more groups per CU, whose loads overlap each other's
+// arithmetic and stores.  Tokens t > 0 reuse the registers; HBM sees the
 // state exactly once in each direction.
 #include "gdn_common.h"
 #include "gdn_hip.h"
@@ -25,7 +28,15 @@ namespace gdn {
 namespace {
 
 constexpr int kDecThreads = 256;
-constexpr int kRowsPerThread = kDK / 8;  // 16
+#ifndef GDN_DEC_SPLIT
+#define GDN_DEC_SPLIT 2
+#endif
+constexpr int kDecSplit = GDN_DEC_SPLIT;      // work-groups per (batch, v-head)
+constexpr int kDecCols = kDV / kDecSplit;     // columns per work-group
+constexpr int kColBlocks = kDecCols / 4;      // 16 column blocks of 4
+constexpr int kRowGroups = kDecThreads / kColBlocks;   // 16
+constexpr int kRowsPerThread = kDK / kRowGroups;       // 8
+static_assert(kRowGroups * kRowsPerThread == kDK && kRowGroups % 4 == 0, "row groups");
 
 // kNorm: q and k rows are raw and normalised here first, x rsqrt(sum x^2 +
 // 1e-6) in fp32 rounded to bf16 (transformers' use_qk_l2norm_in_kernel).
@@ -36,14 +47,15 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
     const float* __restrict__ beta, uint16_t* __restrict__ o, float* __restrict__ state, int T,
     int HV, int HK, float scale) {
     __shared__ float qs[kDK], ks[kDK];
-    __shared__ f32x4 part[4][2][32];  // [wave][a|b][column block]
+    __shared__ f32x4 part[4][2][kColBlocks];  // [wave][a|b][column block]
     __shared__ float kq;
 
     const int tid = threadIdx.x;
-    const int cb = tid & 31;   // column block: columns 4cb .. 4cb+3
-    const int rg = tid >> 5;   // row group: rows rg + 8m
+    const int cb = tid & (kColBlocks - 1);   // column block: columns c0 + 4cb .. + 3
+    const int rg = tid / kColBlocks;         // row group: rows rg + 16m
     const int wave = tid >> 6;
-    const int bh = blockIdx.x;  // b * HV + hv
+    const int bh = blockIdx.x / kDecSplit;  // b * HV + hv
+    const int c0 = kDecCols * (blockIdx.x % kDecSplit);
     const int b = bh / HV, hv = bh - b * HV;
     const int hk = hv / (HV / HK);
 
@@ -56,7 +68,7 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
     auto load_token = [&](int t, uint16_t& qkr, uint2& vr, float& gr, float& br) {
         const size_t tk = (size_t)b * T + t;
         qkr = qk[tk * HK * kDK];
-        vr = *reinterpret_cast<const uint2*>(v + (tk * HV + hv) * kDV + 4 * cb);
+        vr = *reinterpret_cast<const uint2*>(v + (tk * HV + hv) * kDV + c0 + 4 * cb);
         gr = g[tk * HV + hv];
         br = beta[tk * HV + hv];
     };
@@ -71,7 +83,8 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
     f32x4 s[kRowsPerThread];
 #pragma unroll
     for (int m = 0; m < kRowsPerThread; ++m)
-        s[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + (rg + 8 * m) * kDV) + cb);
+        s[m] = __builtin_nontemporal_load(
+            reinterpret_cast<const f32x4*>(S + (rg + kRowGroups * m) * kDV + c0) + cb);
 
     for (int t = 0; t < T; ++t) {
         const size_t tk = ((size_t)b * T + t);
@@ -103,17 +116,20 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
         f32x4 pa = zero4(), pb = zero4();
 #pragma unroll
         for (int m = 0; m < kRowsPerThread; ++m) {
-            const int r = rg + 8 * m;
+            const int r = rg + kRowGroups * m;
             pa += s[m] * ks[r];
             pb += s[m] * qs[r];
         }
-        // lanes l and l+32 of a wave share the column block
+        // the lanes of a wave with one column block (lane % kColBlocks) add up
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pa[i] += __shfl_xor(pa[i], 32, 64);
-            pb[i] += __shfl_xor(pb[i], 32, 64);
+        for (int off = kColBlocks; off < 64; off <<= 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pa[i] += __shfl_xor(pa[i], off, 64);
+                pb[i] += __shfl_xor(pb[i], off, 64);
+            }
         }
-        if ((tid & 63) < 32) {
+        if ((tid & 63) < kColBlocks) {
             part[wave][0][cb] = pa;
             part[wave][1][cb] = pb;
         }
@@ -133,15 +149,15 @@ __global__ __launch_bounds__(kDecThreads) void gdn_recurrent_kernel(
             uint2 packed;
             packed.x = (uint32_t)f32_to_bf16_bits(ov[0]) | ((uint32_t)f32_to_bf16_bits(ov[1]) << 16);
             packed.y = (uint32_t)f32_to_bf16_bits(ov[2]) | ((uint32_t)f32_to_bf16_bits(ov[3]) << 16);
-            *reinterpret_cast<uint2*>(o + (tk * HV + hv) * kDV + 4 * cb) = packed;
+            *reinterpret_cast<uint2*>(o + (tk * HV + hv) * kDV + c0 + 4 * cb) = packed;
         }
 #pragma unroll
-        for (int m = 0; m < kRowsPerThread; ++m) s[m] = s[m] * decay + delta * ks[rg + 8 * m];
+        for (int m = 0; m < kRowsPerThread; ++m) s[m] = s[m] * decay + delta * ks[rg + kRowGroups * m];
         __syncthreads();  // qs/ks/part are rewritten by the next token
     }
 #pragma unroll
     for (int m = 0; m < kRowsPerThread; ++m)
-        __builtin_nontemporal_store(s[m], reinterpret_cast<f32x4*>(S + (rg + 8 * m) * kDV) + cb);
+        __builtin_nontemporal_store(s[m], reinterpret_cast<f32x4*>(S + (rg + kRowGroups * m) * kDV + c0) + cb);
 }
 
 }  // namespace
@@ -159,7 +175,7 @@ hipError_t recurrent_launch(const void* q, const void* k, const void* v, const f
     if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     hipLaunchKernelGGL(norm ? gdn_recurrent_kernel<true> : gdn_recurrent_kernel<false>,
-                       dim3((unsigned)(B * HV)), dim3(kDecThreads), 0, stream,
+                       dim3((unsigned)(kDecSplit * B * HV)), dim3(kDecThreads), 0, stream,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), g, beta, static_cast<uint16_t*>(o), state,
                        T, HV, HQK, 1.0f / sqrtf((float)kDK));
