@@ -76,9 +76,11 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False,
                            cu_seqlens=None, **kwargs):
     """Chunked gated delta rule (prefill).  Returns ``(o, final_state)``,
-    final_state None unless ``output_final_state``."""
+    final_state None unless ``output_final_state``; o has q's dtype, as in
+    transformers' fallback (modeling_qwen3_5.py:326, ``.to(initial_dtype)``)."""
     import torch
 
+    out_dtype = q.dtype
     q, k, v, g, beta, HV, norm = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel,
                                           kernel_norm=True)
     s0 = None
@@ -92,16 +94,18 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                                       qk_l2norm=norm)
     else:
         o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0, qk_l2norm=norm)
-    return o, (sf if output_final_state else None)
+    return o.to(out_dtype), (sf if output_final_state else None)
 
 
 def recurrent_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                                output_final_state=False, use_qk_l2norm_in_kernel=False,
                                cu_seqlens=None, **kwargs):
-    """Token-by-token gated delta rule (decode).  Returns ``(o, final_state)``;
-    the caller's initial_state is not modified."""
+    """Token-by-token gated delta rule (decode).  Returns ``(o, final_state)``
+    with o in q's dtype (modeling_qwen3_5.py:379); the caller's initial_state
+    is not modified."""
     import torch
 
+    out_dtype = q.dtype
     if cu_seqlens is not None:
         raise NotImplementedError("recurrent_gated_delta_rule takes no cu_seqlens here")
     q, k, v, g, beta, HV, norm = _prepare(q, k, v, g, beta, scale, use_qk_l2norm_in_kernel,
@@ -112,4 +116,4 @@ def recurrent_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     else:
         state = initial_state.float().clone().contiguous()
     o = gdn_hip.recurrent_step(q, k, v, g, beta, state, qk_l2norm=norm)
-    return o, (state if output_final_state else None)
+    return o.to(out_dtype), (state if output_final_state else None)

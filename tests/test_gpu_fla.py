@@ -92,6 +92,25 @@ def test_chunk_matches_transformers(fla_ops, torch_ref, dev, B, T, HK, HV):
     _check(o, o_ref, s, s_ref, f"chunk B{B} T{T} HK{HK} HV{HV}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_output_dtype_follows_input(fla_ops, torch_ref, dev, dtype):
+    """fp16 / fp32 layers: o comes back in q's dtype, as transformers' fallback
+    returns it (.to(initial_dtype)), with the same values as the bf16 path."""
+    q, k, v, g, beta, s0 = _layer_inputs(1, 150, 2, 4, seed=21)
+    o_ref, s_ref = torch_ref[0](q.float(), k.float(), v.float(), g, beta, initial_state=s0,
+                                output_final_state=True, use_qk_l2norm_in_kernel=True)
+    args = [t.to(dev, dtype) for t in (q, k, v)] + [t.to(dev) for t in (g, beta)]
+    o, s = fla_ops.chunk_gated_delta_rule(*args, initial_state=s0.to(dev), output_final_state=True,
+                                          use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert o.dtype == dtype and o.shape == v.shape
+    _check(o, o_ref, s, s_ref, f"chunk {dtype}")
+    o1, s1 = fla_ops.recurrent_gated_delta_rule(*[t[:, :1] for t in args], initial_state=s0.to(dev),
+                                                output_final_state=True,
+                                                use_qk_l2norm_in_kernel=True)
+    assert o1.dtype == dtype
+
+
 def test_chunk_varlen_matches_per_sequence(fla_ops, torch_ref, dev):
     lens = [70, 1, 129]
     q, k, v, g, beta, _ = _layer_inputs(1, sum(lens), 2, 4, seed=3)
