@@ -898,8 +898,9 @@ struct ScanSmem {
     StageP p[kRingP];
     Hand h[kHand];
     LoHand lo[kLoSlots];   // after the last chunk: the helper's Sc (8 KB)
-    int fill[2];     // per loader: chunks of its parity whose ring-C loads (and the next
-                     // chunk's ring-P loads) have landed
+    int fill[2];     // per loader: chunks of its parity whose ring-C loads have landed
+    int pfill[2];    // per loader: chunks c of its parity whose next chunk's ring-P loads
+                     // (V, gates of c + 1) have landed
     int uready;      // chunks whose U is in ring P (producer)
     int freeC;       // chunks whose ring-C and ring-P stages the chain has finished reading
     int ready;       // chunks whose hand-off slot the chain has written
@@ -925,6 +926,13 @@ __device__ __forceinline__ int lds_ld(const int* p) {
 }
 __device__ __forceinline__ void lds_st(int* p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// LDS store of a counter, invisible to the compiler's wait placement: use
+// only where an explicit s_waitcnt has already ordered what it publishes.
+__device__ __forceinline__ void lds_st_asm(int* p, int v) {
+    const uint32_t addr = (uint32_t)(size_t)(__attribute__((address_space(3))) int*)p;
+    asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
 }
 
 // Wait until every LDS operation of this wave has completed (lgkmcnt(0)).
@@ -991,12 +999,16 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
 constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
 static_assert(vmcnt_imm(16) == 0x4F70 && vmcnt_imm(0) == 0x0F70, "s_waitcnt encoding");
 
+constexpr int kPLoads = 3;   // direct-to-LDS loads of one ring-P stage (V: 2, gates: 1)
+
 // Loader j (0 or 1) takes the chunks c of parity j: it issues one group of
-// direct-to-LDS loads, ring C for chunk c (K rows: 16, -W: 16) and ring P for
-// chunk c + kLeadP (V: 2, gates: 1), waits for the group and publishes it.
-// Past the sequence's end the ring-P index is clamped, so every group holds
-// the same number of loads.  Loader 0 also loads ring P's lead chunks
-// first, published with its first group.
+// direct-to-LDS loads, ring C for chunk c (K^T: 16, -W: 16) and then ring P
+// for chunk c + kLeadP (V: 2, gates: 1), and publishes each part as it lands
+// (loads complete in order, so ring C is in while ring P's three may still be
+// in flight): V comes from the caller's input, possibly from HBM, and the
+// chain's next step needs only ring C.  Past the sequence's end the ring-P
+// index is clamped, so every group holds the same number of loads.  Loader 0
+// also loads ring P's lead chunk first, in with its first ring-C stage.
 __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                            int j, int lane) {
     auto rows_of = [&](int c) { return min(kChunk, x.len - c * kChunk); };
@@ -1033,10 +1045,17 @@ __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
         // (c + kLeadP) % kRingP held chunk c + kLeadP - kRingP <= c - kRingC
         if (!w.until([&] { return lds_ld(&sm.freeC) >= c - kRingC + 1; })) break;
         asm volatile("" ::: "memory");
-        issue_p(c + kLeadP);
         issue_c(c);
+        asm volatile("" ::: "memory");   // ring P's loads are issued after ring C's
+        issue_p(c + kLeadP);
+        static_assert(kPLoads == 3, "ring P's loads may stay in flight");
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPLoads));   // ring C's 32 loads (and older) are in
+        // The store goes through asm: the compiler places a wait for every
+        // direct-to-LDS load before any LDS access it cannot tell apart from
+        // their destinations, which would hold it back for ring P's loads too.
+        if (lane == 0) lds_st_asm(&sm.fill[j], (c >> 1) + 1);
         vm_wait_all();
-        if (lane == 0) lds_st(&sm.fill[j], (c >> 1) + 1);
+        if (lane == 0) lds_st(&sm.pfill[j], (c >> 1) + 1);
     }
     vm_wait_all();   // no load may land in LDS after the group ends
 }
@@ -1071,10 +1090,14 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
         }
     };
     auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri]) -> bool {
-        // ring P of chunk c landed with loader group c - kLeadP (chunk 0's
-        // lead with loader 0's first group)
-        const int lc = max(c - kLeadP, 0);
-        if (!w.until([&] { return lds_ld(&sm.fill[lc & 1]) >= (lc >> 1) + 1; })) return false;
+        // ring P of chunk c landed with loader group c - kLeadP (pfill); chunk
+        // 0's, issued before loader 0's first ring-C stage, with that (fill)
+        const int lc = c - kLeadP;
+        if (!w.until([&] {
+                return lc < 0 ? lds_ld(&sm.fill[0]) >= 1
+                              : lds_ld(&sm.pfill[lc & 1]) >= (lc >> 1) + 1;
+            }))
+            return false;
         asm volatile("" ::: "memory");
         StageP& st = sm.p[c % kRingP];
         // X = beta V: lane (g, n) of tile mt holds tokens 16 mt + 4 g + i of
@@ -1719,6 +1742,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     if (tid == 0) {
         lds_st(&sm.fill[0], 0);
         lds_st(&sm.fill[1], 0);
+        lds_st(&sm.pfill[0], 0);
+        lds_st(&sm.pfill[1], 0);
         lds_st(&sm.uready, 0);
         lds_st(&sm.freeC, 0);
         lds_st(&sm.ready, 0);
