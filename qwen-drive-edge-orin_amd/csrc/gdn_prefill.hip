@@ -374,6 +374,29 @@ __device__ __forceinline__ void st_through(V* p, const V& v) {
     }
 }
 
+// x + (x moved by one DPP control), sources outside the row and rows outside
+// the row mask contributing 0
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_add(float x) {
+    const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, kRowMask, 0xf,
+                                              true);
+    return x + __builtin_bit_cast(float, t);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (no LDS
+// round trip): row shifts by 1, 2, 4 and 8 within each row of 16 lanes, then
+// lane 15 of rows 0 and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into
+// rows 2 and 3 (row_bcast:31).
+__device__ inline float wave_prefix_sum(float x) {
+    x = dpp_add<0x111, 0xf>(x);   // row_shr:1
+    x = dpp_add<0x112, 0xf>(x);   // row_shr:2
+    x = dpp_add<0x114, 0xf>(x);   // row_shr:4
+    x = dpp_add<0x118, 0xf>(x);   // row_shr:8
+    x = dpp_add<0x142, 0xa>(x);   // row_bcast:15
+    x = dpp_add<0x143, 0xc>(x);   // row_bcast:31
+    return x;
+}
+
 // ---------------------------------------------------------------------------
 // prep kernel: one work-group (4 waves) per (chunk, v-head)
 // ---------------------------------------------------------------------------
@@ -578,13 +601,9 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             gv = 0.f;
             bv = 0.f;
         }
-        float cs = gv;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float o = __shfl_up(cs, off, 64);
-            if (lane >= off) cs += o;
-        }
-        const float c63 = __shfl(cs, 63, 64);
+        const float cs = wave_prefix_sum(gv);
+        const float c63 = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cs), 63));
         sm.cl[lane] = cs * kLog2e;
         sm.b[lane] = bv;
         float* gr = ws.gates + ch * (kGateBytes / 4);
