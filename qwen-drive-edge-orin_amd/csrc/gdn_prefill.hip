@@ -411,6 +411,7 @@ struct PrepSmem {
     float AT[kChunk * kMS];
     float cl[kChunk];   // c * log2(e)
     float b[kChunk];    // beta
+    float bec[kChunk];  // beta e^c
 };
 
 // T[r][c0 .. c0+3] (c0 a multiple of 4) from the in-place inverse layout.
@@ -604,12 +605,15 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         const float cs = wave_prefix_sum(gv);
         const float c63 = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cs), 63));
-        sm.cl[lane] = cs * kLog2e;
+        const float clog = cs * kLog2e;
+        const float ec = __builtin_amdgcn_exp2f(clog);
+        sm.cl[lane] = clog;
         sm.b[lane] = bv;
+        sm.bec[lane] = bv * ec;
         float* gr = ws.gates + ch * (kGateBytes / 4);
         st_through(&gr[kGBeta + lane], bv);
         st_through(&gr[kGDec + lane], lane < rows ? __builtin_amdgcn_exp2f((c63 - cs) * kLog2e) : 0.f);
-        st_through(&gr[kGSec + lane], scale * __builtin_amdgcn_exp2f(cs * kLog2e));
+        st_through(&gr[kGSec + lane], scale * ec);
         st_through(&gr[kGC63 + lane], lane == 0 ? c63 : 0.f);
         if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
     }
@@ -635,9 +639,11 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             case 2: am_products<2>(ka, qf, accA, accM); break;
             default: am_products<3>(ka, qf, accA, accM); break;
         }
-        // A: element (r = 16mt + 4lg + i, col = 16w + lm); the upper part of
-        // column block w is written as zero (every element computed, then
-        // selected: the discarded exponentials may overflow harmlessly)
+        // Element (r = 16mt + 4lg + i, col = 16w + lm) of A (r > col) and
+        // of M^T (key r <= col: M fragment (w, kb) = key tiles 2kb, 2kb+1):
+        // exactly one of the two is nonzero, so one exponential serves both,
+        // e^{c_r - c_col} for A, e^{c_col - c_r} for M; the upper part of A's
+        // column block w and the lower part of M's are written as zero
         const int col = wave * 16 + lm;
         const float ccol = sm.cl[col];
         f32x4 clr[4], br[4];
@@ -646,29 +652,20 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             clr[mt] = *reinterpret_cast<const f32x4*>(&sm.cl[mt * 16 + 4 * lg]);
             br[mt] = *reinterpret_cast<const f32x4*>(&sm.b[mt * 16 + 4 * lg]);
         }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = mt * 16 + 4 * lg + i;
-                const float av = -br[mt][i] * accA[mt][i] * __builtin_amdgcn_exp2f(clr[mt][i] - ccol);
-                const float a = r > col ? av : 0.f;
-                sm.AT[r * kMS + col] = a;
-                if (kDbg) ws.dbgA[ch * kChunk * kChunk + r * kChunk + col] = a;
-            }
-        }
-        // M^T tile (key tile mt, query tile w): element (key = 16mt + 4lg + i,
-        // query = col); M fragment (w, kb) = key tiles 2kb, 2kb+1
         half4 mh[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             f32x4 val;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int key = mt * 16 + 4 * lg + i;
-                const float mv = scale * accM[mt][i] * __builtin_amdgcn_exp2f(ccol - clr[mt][i]);
-                val[i] = key <= col ? mv : 0.f;
-                if (kDbg) ws.dbgM[ch * kChunk * kChunk + col * kChunk + key] = val[i];
+                const int r = mt * 16 + 4 * lg + i;
+                const bool lower = r > col;
+                const float e = __builtin_amdgcn_exp2f(lower ? clr[mt][i] - ccol : ccol - clr[mt][i]);
+                const float a = lower ? -br[mt][i] * accA[mt][i] * e : 0.f;
+                sm.AT[r * kMS + col] = a;
+                if (kDbg) ws.dbgA[ch * kChunk * kChunk + r * kChunk + col] = a;
+                val[i] = lower ? 0.f : scale * accM[mt][i] * e;
+                if (kDbg) ws.dbgM[ch * kChunk * kChunk + col * kChunk + r] = val[i];
             }
             mh[mt] = to_half4(val);
         }
@@ -823,13 +820,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int c0 = 32 * kb + 16 * hh + 4 * lg;
-                const f32x4 bb = *reinterpret_cast<const f32x4*>(&sm.b[c0]);
-                const f32x4 cc = *reinterpret_cast<const f32x4*>(&sm.cl[c0]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) bec[kb][hh][e] = bb[e] * __builtin_amdgcn_exp2f(cc[e]);
-            }
+            for (int hh = 0; hh < 2; ++hh)
+                bec[kb][hh] = *reinterpret_cast<const f32x4*>(&sm.bec[32 * kb + 16 * hh + 4 * lg]);
         }
         half8* wdst = ws.W + ch * (16 * 64);
 #pragma unroll
