@@ -661,10 +661,13 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                 const int r = mt * 16 + 4 * lg + i;
                 const bool lower = r > col;
                 const float e = __builtin_amdgcn_exp2f(lower ? clr[mt][i] - ccol : ccol - clr[mt][i]);
-                const float a = lower ? -br[mt][i] * accA[mt][i] * e : 0.f;
+                // both products, then selects: no branch per element
+                float av = -br[mt][i] * accA[mt][i] * e, mv = scale * accM[mt][i] * e;
+                asm volatile("" : "+v"(av), "+v"(mv));
+                const float a = lower ? av : 0.f;
                 sm.AT[r * kMS + col] = a;
                 if (kDbg) ws.dbgA[ch * kChunk * kChunk + r * kChunk + col] = a;
-                val[i] = lower ? 0.f : scale * accM[mt][i] * e;
+                val[i] = lower ? 0.f : mv;
                 if (kDbg) ws.dbgM[ch * kChunk * kChunk + col * kChunk + r] = val[i];
             }
             mh[mt] = to_half4(val);
