@@ -102,7 +102,7 @@ struct Workspace {
     float* gates;       // [chunk-head][256]
     half8* Q;           // Q fragments [chunk * HK + hk][mt * 4 + kb][64]
     u32x4* KT;          // K^T bf16 fragments [chunk * HK + hk][t * 2 + kb][64]
-    uint32_t* ssq;      // [chunk-head][slice][64] fp32 bits, sign bit set = not yet written
+    uint32_t* ssq;      // [chunk-head][slice][64] fp32 bits, sign bit set = not yet written (null outside the norm epilogue)
     unsigned* status;   // bit 0: a bounded wait gave up
     float* dbgT;        // optional [chunk-head][64][64]: T = (I - A)^-1
     float* dbgA;        // optional: A
@@ -483,8 +483,9 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         return;
     (void)seq;
     const size_t ch = (size_t)cid * HV + hv;
-    // this call's gated-RMSNorm slots start invalid (2 KB: 16 bytes a thread)
-    if (tid < kSlices * kChunk / 4)
+    // this call's gated-RMSNorm slots start invalid (2 KB: 16 bytes a
+    // thread; only when the scan runs the norm epilogue)
+    if (ws.ssq && tid < kSlices * kChunk / 4)
         st_through(reinterpret_cast<u32x4*>(ws.ssq + ch * (kSlices * kChunk)) + tid,
                    u32x4{~0u, ~0u, ~0u, ~0u});
 
@@ -1829,7 +1830,7 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     ws.gates = reinterpret_cast<float*>(base + L.gates);
     ws.Q = reinterpret_cast<half8*>(base + L.q);
     ws.KT = reinterpret_cast<u32x4*>(base + L.kt);
-    ws.ssq = reinterpret_cast<uint32_t*>(base + L.ssq);
+    ws.ssq = norm ? reinterpret_cast<uint32_t*>(base + L.ssq) : nullptr;   // norm epilogue only
     ws.status = reinterpret_cast<unsigned*>(base);
     if (dump_debug) {
         ws.dbgT = reinterpret_cast<float*>(base + L.dbgT);
