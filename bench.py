@@ -38,6 +38,26 @@ def _bytes(*ts):
     return sum(t.numel() * t.element_size() for t in ts if t is not None)
 
 
+def whole_call_roofline(flops, algo_bytes, ms):
+    """Fractions of the whole call against both bounds, and the attainable
+    rate min(MFMA peak, AI x HBM peak) with AI = algorithmic FLOPs / minimum
+    unique HBM bytes: the best a call can do when it reads its inputs and
+    writes its outputs once at peak bandwidth."""
+    tflops = flops / ms / 1e9
+    gbs = algo_bytes / ms / 1e6
+    ai = flops / algo_bytes
+    attain = min(MFMA_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1e3)
+    return {"mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "algo_flops": flops, "algo_bytes": algo_bytes,
+            "arith_intensity_flop_per_byte": round(ai, 1),
+            "ridge_flop_per_byte": round(MFMA_PEAK_TFLOPS * 1e3 / HBM_PEAK_GBS, 1),
+            "attainable_tflops": round(attain, 1),
+            "attainable_bound": "hbm" if ai * HBM_PEAK_GBS / 1e3 < MFMA_PEAK_TFLOPS else "mfma",
+            "attainable_us": round(flops / attain / 1e6, 3),
+            "frac_of_attainable": round(tflops / attain, 4)}
+
+
 def time_calls(fn, n_sets, steps, warmup):
     """HIP-event time of `steps` back-to-back calls fn(i) on the current
     stream, bracketed by device synchronisation; returns ms per call."""
@@ -112,9 +132,10 @@ def bench_prefill(ops, dev, steps, warmup):
 
 
 def bench_prefill_norm(ops, dev, steps, warmup):
-    """The prefill with the gated RMSNorm in its output stage (chunk_prefill_norm)
-    at T=1141 HV=32, cold inputs, against the two steps it replaces
-    (chunk_prefill, then gated_rmsnorm) on the same rotated inputs."""
+    """The prefill with the gated RMSNorm in its output stage
+    (chunk_prefill_norm(fused=True)) at T=1141 HV=32, cold inputs, against the
+    two steps it replaces (chunk_prefill, then gated_rmsnorm; what
+    chunk_prefill_norm runs by default) on the same rotated inputs."""
     import torch
     import gdn_cases as gc
 
@@ -125,7 +146,8 @@ def bench_prefill_norm(ops, dev, steps, warmup):
     per = _bytes(q, k, v, g, beta, s0, z)
     sets = rotation(lambda: (q, k, v, g, beta, s0, z, w), per, dev)
     ms_f = time_calls(lambda i: ops.chunk_prefill_norm(*sets[i][:5], sets[i][6], sets[i][7],
-                                                       sets[i][5]), len(sets), steps, warmup)
+                                                       sets[i][5], fused=True),
+                      len(sets), steps, warmup)
 
     def two(i):
         o, _ = ops.chunk_prefill(*sets[i][:6])
@@ -310,15 +332,17 @@ def bench_conv(ops, dev, steps, warmup):
 # Algorithmic FLOPs per chunk-head of each prefill kernel under the fixed
 # convention (C = 64, dk = dv = 128, 2 FLOP per MAC; five C x C x 128
 # products, three 64 x 128 x 128 products and C^3/3 MACs of inversion, 182.95
-# kFLOP per token per v-head in total): prep forms K K^T, Q K^T and the
-# inversion; scan forms the rest -- the T (v beta) and T (k beta e^c) terms
-# (here T R with R = beta V - beta e^c K S), W S (here K S), (Q e^c) S,
-# K~^T V_new and M V_new.
+# kFLOP per token per v-head in total), split by where each product runs:
+#   prep  K K^T, Q K^T, W = T diag(beta e^c) K, and the inversion
+#         = 3 C x C x 128 + C^3/3 = 3.32 MFLOP
+#   scan  U = T diag(beta) V, M V_new (two C x C x 128), W S, (Q e^c) S and
+#         K~^T V_new (three 64 x 128 x 128) = 8.39 MFLOP
 _CC = 2 * 64 * 64 * 128          # one C x C x 128 product
 _CD = 2 * 64 * 128 * 128         # one 64 x 128 x 128 product
 _INV = 2 * 64 ** 3 // 3
-KERNEL_FLOPS_PER_CHUNK_HEAD = {"gdn_prep_kernel": 2 * _CC + _INV,
-                               "gdn_scan_kernel": 3 * _CD + 3 * _CC}
+KERNEL_FLOPS_PER_CHUNK_HEAD = {"gdn_prep_kernel": 3 * _CC + _INV,
+                               "gdn_scan_kernel": 3 * _CD + 2 * _CC}
+assert sum(KERNEL_FLOPS_PER_CHUNK_HEAD.values()) == 5 * _CC + 3 * _CD + _INV
 
 
 class _Hip:
@@ -356,11 +380,13 @@ class _Hip:
 
 
 def kernel_times(dev, steps, warmup):
-    """Average duration of each prefill kernel at T=1141 HV=32: `steps`
+    """Average duration of each prefill kernel at T=1141 HV=32, cold: `steps`
     back-to-back launches of that kernel alone (deltanet_chunk_prefill_kernel)
-    between two HIP events on the launch stream.  The prep launches rotate over
-    the cold input copies; the scan launches reread a workspace that a full
-    call filled for the same inputs, as the scan does right after the prep."""
+    between two HIP events on the launch stream.  Every launch touches inputs
+    and a workspace the previous launches did not: the launches rotate over the
+    resident input copies, each with its own workspace, which a full call
+    filled beforehand for the scan's launches (the scan reads the records the
+    prep of the same inputs wrote)."""
     import torch
     import gdn_cases as gc
     from gdn_hip import capi
@@ -373,8 +399,8 @@ def kernel_times(dev, steps, warmup):
     B, T, HK, D = q.shape
     HV = v.shape[2]
     sets = rotation(lambda: (q, k, v, g, beta, s0), _bytes(q, k, v, g, beta, s0), dev)
-    wsb = lib.deltanet_prefill_workspace_size(B, T, HV, D, D, 64)
-    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    wsb = lib.deltanet_prefill_live_workspace_size(B, T, HV, D, D, 64)
+    wss = [torch.empty(wsb, dtype=torch.uint8, device=dev) for _ in sets]
     o = torch.empty_like(sets[0][2])
     sf = torch.empty_like(sets[0][5])
     stream = torch.cuda.current_stream().cuda_stream
@@ -383,7 +409,7 @@ def kernel_times(dev, steps, warmup):
         qq, kk, vv, gg, bb, ss = sets[i % len(sets)]
         args = (qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), gg.data_ptr(), bb.data_ptr(),
                 o.data_ptr(), ss.data_ptr(), sf.data_ptr(), B, T, HV, HK, D, D, 64,
-                ws.data_ptr(), wsb, stream)
+                wss[i % len(sets)].data_ptr(), wsb, stream)
         err = (lib.deltanet_chunk_prefill(*args, 0) if kernel < 0
                else lib.deltanet_chunk_prefill_kernel(*args, kernel))
         assert err == 0, f"prefill kernel {kernel} returned {err}"
@@ -391,21 +417,22 @@ def kernel_times(dev, steps, warmup):
     out = {}
     nch = B * ((T + 63) // 64) * HV
     for j, nm in enumerate(names):
-        scan_like = j > 0
-        if scan_like:
-            launch(0, -1)   # workspace of set 0
+        if j > 0:
+            for i in range(len(sets)):
+                launch(i, -1)   # every workspace holds its inputs' records
         for i in range(warmup):
-            launch(0 if scan_like else i, j)
+            launch(i, j)
         torch.cuda.synchronize()
         ev = hip.events(2)
         hip.record(ev[0], stream)
         for i in range(steps):
-            launch(0 if scan_like else i, j)
+            launch(i, j)
         hip.record(ev[1], stream)
         torch.cuda.synchronize()
         out[nm] = dict(ms=hip.elapsed_ms(ev[0], ev[1]) / steps,
                        flops=KERNEL_FLOPS_PER_CHUNK_HEAD[nm] * nch)
         hip.destroy(ev)
+    del wss
     return out
 
 
@@ -603,10 +630,7 @@ def main():
                    "inputs": f"rotated over {pre['n_sets']} resident copies (cold)"},
         "warm": {"us_per_call": round(pre["warm_ms"] * 1e3, 2),
                  "tflops": round(pre["flops"] / pre["warm_ms"] / 1e9, 3)},
-        "roofline_whole_call": {
-            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
-            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "algo_flops": pre["flops"], "algo_bytes": pre["algo_bytes"]},
+        "roofline_whole_call": whole_call_roofline(pre["flops"], pre["algo_bytes"], ms),
     }
     kt = kernel_times(dev, args.steps, args.warmup)
     trace = trace_from_profiles()
@@ -615,15 +639,25 @@ def main():
     dom = max(kt, key=lambda nm: trace.get(nm, kt[nm]["ms"] * 1e3))
     per = {}
     for nm, d in kt.items():
-        ach = d["flops"] / d["ms"] / 1e9
-        per[nm] = {"us_per_launch": round(d["ms"] * 1e3, 2), "trace_avg_us": trace.get(nm),
-                   "achieved": round(ach, 3), "frac": round(ach / MFMA_PEAK_TFLOPS, 5),
-                   "algo_flops": d["flops"], "traffic": traffic_from_profiles(nm)}
+        # achieved / frac from the committed rocprof trace average (each
+        # launch's own begin-to-end time); the live back-to-back cold figure
+        # beside it (it also counts the launch gaps between kernels)
+        live = d["flops"] / d["ms"] / 1e9
+        t_us = trace.get(nm)
+        ach = d["flops"] / t_us / 1e6 if t_us else live
+        per[nm] = {"trace_avg_us": t_us, "achieved": round(ach, 3),
+                   "frac": round(ach / MFMA_PEAK_TFLOPS, 5),
+                   "us_per_launch_live": round(d["ms"] * 1e3, 2),
+                   "achieved_live": round(live, 3), "frac_live": round(live / MFMA_PEAK_TFLOPS, 5),
+                   "algo_flops": d["flops"],
+                   "algo_flops_per_chunk_head": KERNEL_FLOPS_PER_CHUNK_HEAD[nm],
+                   "traffic": traffic_from_profiles(nm)}
     line["roofline"] = {
         "kernel": dom, "bound": "mfma", "achieved": per[dom]["achieved"],
         "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": per[dom]["frac"],
-        "traffic": per[dom]["traffic"], "us_per_launch": per[dom]["us_per_launch"],
-        "kernels_us": {nm: round(d["ms"] * 1e3, 2) for nm, d in kt.items()},
+        "traffic": per[dom]["traffic"], "trace_avg_us": per[dom]["trace_avg_us"],
+        "us_per_launch_live": per[dom]["us_per_launch_live"],
+        "frac_live": per[dom]["frac_live"],
         "kernels": per,
     }
     if not args.no_secondary:

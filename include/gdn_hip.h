@@ -55,6 +55,13 @@ hipError_t deltanet_chunk_prefill_noalloc(const void* q, const void* k, const vo
                                           int T, int HV, int HQK, int DK, int DV, int chunk_size,
                                           hipStream_t stream);
 
+/* deltanet_prefill_status for the array deltanet_chunk_prefill_noalloc uses
+ * on the current device: synchronises `stream`, then returns hipSuccess, or
+ * hipErrorLaunchTimeOut when a bounded wait of the last allocation-free call
+ * on this device gave up.  Allocates nothing.  No counterpart in the
+ * reference (for the same callers as deltanet_chunk_prefill_noalloc). */
+hipError_t deltanet_prefill_noalloc_status(hipStream_t stream);
+
 /* Workspace bytes for dump_debug = 0 only (no counterpart in the reference,
  * whose size always includes its debug regions): a 256-byte header with the
  * status word, then 69 KB per (chunk, v-head). */
@@ -122,17 +129,15 @@ hipError_t deltanet_chunk_prefill_fused(const void* q, const void* k, const void
                                         int HV, int HQK, int io_dtype, void* workspace,
                                         size_t workspace_bytes, hipStream_t stream);
 
-/* Prefill with the gated RMSNorm fused into its output stage (the reference
- * runs that post-op as a separate TensorRT plugin, kernel::gatedRmsNormForward,
+/* Prefill followed by the gated RMSNorm (the reference runs that post-op as a
+ * separate TensorRT plugin, kernel::gatedRmsNormForward,
  * export/patches/orin_text_engine/files/cpp/kernels/gatedRmsNorm/gatedRmsNormKernel.h:17-18,
  * after the prefill).  Same arguments as deltanet_chunk_prefill (dump_debug = 0)
  * plus z (bf16 [B, T, HV, 128]), norm_weight (bf16 [128]) and eps; y (bf16
  * [B, T, HV, 128]) receives gated_rmsnorm(o, z) = bf16(bf16(w * bf16(o *
  * rsqrt(mean(o^2) + eps))) * silu(z)), o being the bf16 output of
- * deltanet_chunk_prefill, and o itself is never stored.  The fused path runs
- * when the whole scan grid (8 * B * HV work-groups, rounded up) is resident
- * at once; otherwise the prefill writes o into y and the gated RMSNorm rewrites
- * it in place.  Workspace as for deltanet_chunk_prefill. */
+ * deltanet_chunk_prefill: the prefill writes o into y and the gated RMSNorm
+ * kernel rewrites it in place.  Workspace as for deltanet_chunk_prefill. */
 hipError_t deltanet_chunk_prefill_norm(const void* q, const void* k, const void* v,
                                        const float* g, const float* beta, const void* z,
                                        const void* norm_weight, float eps, void* y,
@@ -140,6 +145,25 @@ hipError_t deltanet_chunk_prefill_norm(const void* q, const void* k, const void*
                                        int T, int HV, int HQK, int DK, int DV, int chunk_size,
                                        void* workspace, size_t workspace_bytes,
                                        hipStream_t stream);
+
+/* deltanet_chunk_prefill_norm with the gated RMSNorm fused into the scan's
+ * output stage, so o is never stored (no counterpart in the reference).  The
+ * 8 work-groups that share a row's 128 columns wait on each other's sums of
+ * squares, so the scan is launched cooperatively -- the runtime starts it only
+ * with every group resident -- when the runtime's occupancy figure says the
+ * grid (8 * B * HV groups, rounded up to 64) fits the device at once;
+ * otherwise this runs deltanet_chunk_prefill_norm's two kernels.  A wait that
+ * still gives up (bounded, ~0.1 s) leaves y incomplete and sets the status
+ * word deltanet_prefill_status reports.  Same arguments and results as
+ * deltanet_chunk_prefill_norm; a row's rsqrt may differ from it in the last
+ * bit (the row sum is associated differently). */
+hipError_t deltanet_chunk_prefill_norm_fused(const void* q, const void* k, const void* v,
+                                             const float* g, const float* beta, const void* z,
+                                             const void* norm_weight, float eps, void* y,
+                                             const float* initial_state, float* final_state,
+                                             int B, int T, int HV, int HQK, int DK, int DV,
+                                             int chunk_size, void* workspace,
+                                             size_t workspace_bytes, hipStream_t stream);
 
 /* Variable-length prefill (no counterpart in the reference kernel: its torch
  * fallback drops cu_seqlens, transformers modeling_qwen3_5.py:259).

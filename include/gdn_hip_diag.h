@@ -66,6 +66,21 @@ int deltanet_varlen_chunk_map(const int32_t* cu_seqlens, int num_seqs, int total
                               int32_t* seq_first_chunk, int32_t* seq_chunk_count,
                               int32_t* seq_first_token, int32_t* seq_token_count);
 
+/* Host twins of the kernels' block-cooperative lookups over a packed batch
+ * (host memory, no GPU involved), run phase by phase for `nt` simulated
+ * threads with the kernels' shared arithmetic (gdn_seq.h):
+ *   deltanet_varlen_chunks_before  the scan's chunk count of sequences
+ *       [0, upto) (saturating at 2^30), nt a multiple of 64 up to 1024;
+ *   deltanet_varlen_locate_chunk   the prep's global chunk id -> sequence,
+ *       first token and row count, written to seq_tok_rows[0..2]; returns 1
+ *       when found, 0 when the chunk does not exist, nt a power of two up to
+ *       1024 (the prep runs 256).
+ * Both return -1 for invalid arguments. */
+int deltanet_varlen_chunks_before(const int32_t* cu_seqlens, int num_seqs, int total_tokens,
+                                  int upto, int nt);
+int deltanet_varlen_locate_chunk(const int32_t* cu_seqlens, int num_seqs, int total_tokens,
+                                 int cid, int nt, int32_t* seq_tok_rows);
+
 /* HBM streaming probe (benchmarks only): kind 0 reads a and b and writes
  * c = a ^ b, `bytes` each (three streams, the gated RMSNorm's pattern);
  * kind 1 reads and rewrites c in place (the decode state's pattern).

@@ -23,17 +23,18 @@
 //         substitution, off-diagonal blocks on fp32 MFMA), then -W (fp16,
 //         from W^T = K^T (T diag(beta e^c))^T on fp16 MFMA), T - I as an
 //         fp16 hi / lo pair, M, a gates record, and Q as fp16 fragments.
-//   scan  one work-group per (16 value columns, v-head, sequence), four
-//         waves on four SIMDs: a chain wave keeps the 128 x 16 state slice
-//         in registers and per chunk forms V_n = U - W S (fp16 MFMA, U the
+//   scan  one work-group per (16 value columns, v-head, sequence), eight
+//         specialised waves: a chain wave keeps the 128 x 16 state slice in
+//         registers and per chunk forms V_n = U - W S (fp16 MFMA, U the
 //         accumulator's fp32 initial value) and S <- e^{c63} S + K^T (d V_n)
-//         (bf16 MFMA on the input K, d V_n as a bf16 hi / lo pair, the lo
-//         part into a second accumulator off the serial path); a producer
-//         wave forms U = beta V + (T - I)(beta V) from hi / lo fp16 products;
-//         an output wave forms O; a loader wave moves K, -W, V and the gates
-//         into a three-stage LDS ring with direct-to-LDS loads.  Waves meet
-//         through LDS counters with bounded waits; a wait that runs out aborts
-//         the work-group and sets the workspace's status word
+//         (bf16 MFMA on the input K, d V_n as a bf16 hi / lo pair); a lo
+//         helper wave adds the lo part into a second accumulator off the
+//         serial path; a producer wave forms U = beta V + (T - I)(beta V)
+//         from hi / lo fp16 products; two output waves form O; two loader
+//         waves move K^T, -W, V and the gates into LDS rings with
+//         direct-to-LDS loads; a norm wave serves the gated-RMSNorm epilogue.
+//         Waves meet through LDS counters with bounded waits; a wait that runs
+//         out aborts the work-group and sets the workspace's status word
 //         (deltanet_prefill_status).
 //
 // Rounding budget (checked against an fp64 emulation of each operand class):
@@ -54,8 +55,8 @@
 #include <math.h>
 
 #include <algorithm>
-#include <atomic>
 #include <mutex>
+#include <vector>
 
 namespace gdn {
 namespace {
@@ -263,17 +264,10 @@ __device__ __forceinline__ void kt_reads(const uint16_t* base, int t, int kb, in
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
-// Block-cooperative sequence lookups (clamped cu_seqlens, gdn_seq.h)
+// Block-cooperative sequence lookups (clamped cu_seqlens, gdn_seq.h).  Their
+// host twins (deltanet_varlen_chunks_before / deltanet_varlen_locate_chunk)
+// run the same phases thread by thread, for tests on the CPU.
 // ---------------------------------------------------------------------------
-// Prefix sums of chunk counts saturate at kSatChunks, far above any chunk
-// bound a workspace can hold, so even adversarial cu_seqlens cannot wrap them.
-constexpr int kSatChunks = 1 << 30;
-
-__host__ __device__ inline int sat_add(int a, int b) {
-    const long long s = (long long)a + b;
-    return s > kSatChunks ? kSatChunks : (int)s;
-}
-
 // Number of chunks in sequences [0, upto) (saturating); every thread calls it.
 template <int NT>
 __device__ int chunks_before(const int32_t* cu, int T, int total, int upto, int* red) {
@@ -291,7 +285,11 @@ __device__ int chunks_before(const int32_t* cu, int T, int total, int upto, int*
 }
 
 // Global chunk id -> (sequence, first token, rows); false (uniformly) when cid
-// is past the last chunk.  `red` holds NT ints of scratch.
+// is past the last chunk.  `red` holds NT ints of scratch.  Sequences are
+// taken NT at a time: an inclusive scan of their chunk counts, the one
+// sequence whose range holds cid (at most one: the ranges are disjoint)
+// posts itself, and seq_chunk_rows validates what was posted, so a result is
+// in bounds even where no sequence posted (a saturated prefix).
 template <int NT>
 __device__ bool locate_chunk(const int32_t* cu, int N, int T, int total, int cid, int* red,
                              int& seq, int& tok0, int& rows) {
@@ -304,39 +302,42 @@ __device__ bool locate_chunk(const int32_t* cu, int N, int T, int total, int cid
         rows = min(kChunk, T - c * kChunk);
         return true;
     }
+    const int tid = (int)threadIdx.x;
     int base = 0;
     bool found = false;
     for (int s0 = 0; s0 < N && base < kSatChunks; s0 += NT) {
-        const int s = s0 + (int)threadIdx.x;
+        const int s = s0 + tid;
         const int cnt = (s < N) ? seq_chunks(cu, T, total, s) : 0;
         __syncthreads();
-        red[threadIdx.x] = cnt;
+        red[tid] = cnt;
         __syncthreads();
         for (int off = 1; off < NT; off <<= 1) {
-            const int add = (threadIdx.x >= (unsigned)off) ? red[threadIdx.x - off] : 0;
+            const int v = scan_step(red, tid, off);
             __syncthreads();
-            red[threadIdx.x] = sat_add(red[threadIdx.x], add);
+            red[tid] = v;
             __syncthreads();
         }
-        const int incl = red[threadIdx.x];
+        const int incl = red[tid];
         const int blk = red[NT - 1];
-        const int excl = incl - cnt;   // exact wherever incl has not saturated
         __syncthreads();
-        if (cnt > 0 && incl < kSatChunks && cid >= base + excl && cid < base + incl) {
-            red[0] = s;
-            red[1] = cid - base - excl;
+        if (tid == 0) {   // no sequence has posted yet
+            red[0] = -1;
+            red[1] = -1;
         }
         __syncthreads();
-        if (cid < sat_add(base, blk)) {
+        if (owns_chunk(cnt, incl, base, cid)) {
+            red[0] = s;
+            red[1] = cid - base - (incl - cnt);
+        }
+        __syncthreads();
+        const bool here = cid < sat_add(base, blk);
+        if (here) {
             seq = red[0];
-            const int c = red[1];
-            tok0 = seq_lo(cu, T, total, seq) + c * kChunk;
-            rows = min(kChunk, seq_count(cu, T, total, seq) - c * kChunk);
-            found = true;
+            found = seq_chunk_rows(cu, N, T, total, seq, red[1], tok0, rows);
         }
         __syncthreads();
         base = sat_add(base, blk);
-        if (found) break;
+        if (here) break;
     }
     return found;
 }
@@ -847,29 +848,30 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan kernel: one work-group (6 waves) per (16 value columns, v-head,
+// scan kernel: one work-group (8 waves) per (16 value columns, v-head,
 // sequence).
 //
 // State layout of the chain: accumulator tile t (0..7), lane (g, n), element
 // i holds S[dk][16 sl + n] with dk = 32 (t/2) + 8 g + 4 (t%2) + i, so the
 // fp16 B operand of k-block kb (tiles 2kb, 2kb+1) holds dk 32 kb + 8 g + 0..7
 // in order, matching the -W row-piece fragments, and the K^T operand that
-// produces tile t is two transposing LDS reads of K rows.
+// produces tile t is the prep's K^T fragment pair (t * 2 + kb) of the chunk.
 //
-//   chain     wave 0: V_n = U + (-W) S16 (16 fp16 MFMA), d V_n -> bf16 hi / lo,
-//             S' = e^{c63} S + K^T hi (16 bf16 MFMA), then Sc <- e^{c63} Sc
-//             + K^T lo (16 bf16 MFMA) off the serial path: those products
-//             run in the matrix pipe while the wave hands off, publishes and
-//             reads the next chunk's operands.
+//   chain     wave 0: V_n = U + (-W) S16 (16 fp16 MFMA), d V_n -> bf16 hi,
+//             S' = e^{c63} S + K^T hi (16 bf16 MFMA), d V_n handed to the lo
+//             helper (the debug build does the helper's products here).
 //   producer  wave 1: U = beta V + (T - I)(beta V) with the product as
 //             hi/hi + hi/lo + lo/hi fp16 MFMAs (18), into ring P.
 //   output    waves 2 and 3, chunks of even and odd index:
 //             O^T = (S^T Q^T) diag(s e^c) + V_n^T M^T, with Q, M and s e^c
 //             loaded to registers as soon as the wave's previous chunk has
 //             read them, two chain steps before they are needed.
-//   prefetch  wave 4: L2 warm-up loads kPf chunks ahead of the chain.
+//   norm      wave 4: the gated-RMSNorm epilogue's row sums across the 8
+//             slice groups (norm epilogue only; otherwise it exits at once).
+//   lo helper wave 7: Sc <- e^{c63} Sc + K^T lo, the lo part of the state
+//             update, off the chain's serial path.
 //   loaders   waves 6 and 5, chunks of even and odd index: direct-to-LDS
-//             loads of chunk c's K rows and -W into ring C (3 stages, 32 KB
+//             loads of chunk c's K^T fragments and -W into ring C (3 stages, 32 KB
 //             each) and of chunk c + 1's V and gates record into ring P (4
 //             stages, 7 KB each).  Each loader has one chunk in flight and
 //             publishes it as soon as it lands, so the two keep two chunks in
@@ -1812,6 +1814,14 @@ struct NormIn {
     float eps;
 };
 
+// Scan work-groups of a call over N sequences of HV heads.
+inline long long scan_groups(int N, int HV) {
+    return (long long)((N * HV + 7) / 8) * 8 * kSlicesPerHead;
+}
+
+// The norm epilogue's work-groups wait on each other, so its scan is launched
+// cooperatively (all groups resident at once, or no launch at all); norm !=
+// nullptr requires it.
 hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
@@ -1877,17 +1887,39 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
         sa.nw = norm->w;
         sa.eps = norm->eps;
     }
-    const int pairs = N * HV;
-    const int grp = (pairs + 7) / 8;
-    auto scan = norm ? gdn_scan_kernel<0, false, true>
-                : raw == 1 ? gdn_scan_kernel<1, false>
-                : raw == 2 ? gdn_scan_kernel<2, false>
-                : dump_debug ? gdn_scan_kernel<0, true> : gdn_scan_kernel<0, false>;
-    hipLaunchKernelGGL(scan, dim3((unsigned)(grp * 8 * kSlicesPerHead)), dim3(kScanThreads), 0,
-                       stream, sa);
-    hipError_t err = hipGetLastError();
+    const unsigned grid = (unsigned)scan_groups(N, HV);
+    hipError_t err;
+    if (norm) {
+        void* kargs[] = {&sa};
+        err = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(gdn_scan_kernel<0, false, true>),
+                                         dim3(grid), dim3(kScanThreads), kargs, 0, stream);
+    } else {
+        auto scan = raw == 1 ? gdn_scan_kernel<1, false>
+                    : raw == 2 ? gdn_scan_kernel<2, false>
+                    : dump_debug ? gdn_scan_kernel<0, true> : gdn_scan_kernel<0, false>;
+        hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), 0, stream, sa);
+        err = hipGetLastError();
+    }
     if (ev) (void)hipEventRecord(ev[2], stream);
     return err;
+}
+
+// Whether `groups` work-groups of the norm epilogue's scan fit on the current
+// device at once (the occupancy the runtime reports for that kernel), and the
+// device supports cooperative launches.
+bool norm_scan_coresident(long long groups) {
+    int dev = 0, coop = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
+        !coop)
+        return false;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return false;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(gdn_scan_kernel<0, false, true>), kScanThreads,
+            0) != hipSuccess)
+        return false;
+    return groups <= (long long)per_cu * cus;
 }
 
 constexpr int kPrefillKernels = 2;
@@ -1944,19 +1976,30 @@ extern "C" hipError_t deltanet_chunk_prefill(const void* q, const void* k, const
 }
 
 namespace {
-// Compute units of the current device, queried once per device.
-int device_cus() {
-    constexpr int kDevs = 64;
-    static std::atomic<int> cache[kDevs];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 0;
-    int n = cache[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            return 0;
-        cache[dev].store(n, std::memory_order_relaxed);
-    }
-    return n;
+bool norm_args_ok(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const void* z, const void* norm_weight, float eps, void* y, float* final_state,
+                  int B, int T, int HV, int HQK, int DK, int DV, int chunk_size,
+                  void* workspace) {
+    if (!dims_ok(HV, HQK, DK, DV, chunk_size) || B <= 0 || T < 0) return false;
+    if (workspace == nullptr || final_state == nullptr) return false;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !z || !norm_weight || !y)) return false;
+    return eps >= 0.f;
+}
+
+// The prefill writes o into y, then the gated RMSNorm kernel rewrites it in
+// place: two kernels that never wait on each other.
+hipError_t prefill_then_norm(const void* q, const void* k, const void* v, const float* g,
+                             const float* beta, const void* z, const void* norm_weight, float eps,
+                             void* y, const float* initial_state, float* final_state, int B,
+                             int T, int HV, int HQK, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    hipError_t e = launch_prefill(plain_in(q, k, v, g, beta), 0, y, initial_state, final_state,
+                                  nullptr, B, T, B * T, HV, HQK, nc, workspace, workspace_bytes,
+                                  stream, 0);
+    if (e != hipSuccess || T == 0) return e;
+    return gdn_gated_rmsnorm_forward(y, z, norm_weight, y, (int64_t)B * T * HV, kDV, eps,
+                                     GDN_DTYPE_BF16, GDN_DTYPE_BF16, stream);
 }
 }  // namespace
 
@@ -1967,29 +2010,34 @@ extern "C" hipError_t deltanet_chunk_prefill_norm(const void* q, const void* k, 
                                                   int B, int T, int HV, int HQK, int DK, int DV,
                                                   int chunk_size, void* workspace,
                                                   size_t workspace_bytes, hipStream_t stream) {
-    if (!dims_ok(HV, HQK, DK, DV, chunk_size) || B <= 0 || T < 0) return hipErrorInvalidValue;
-    if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
-    if (T > 0 && (!q || !k || !v || !g || !beta || !z || !norm_weight || !y))
+    if (!norm_args_ok(q, k, v, g, beta, z, norm_weight, eps, y, final_state, B, T, HV, HQK, DK,
+                      DV, chunk_size, workspace))
         return hipErrorInvalidValue;
-    if (!(eps >= 0.f)) return hipErrorInvalidValue;
-    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
+    return prefill_then_norm(q, k, v, g, beta, z, norm_weight, eps, y, initial_state, final_state,
+                             B, T, HV, HQK, workspace, workspace_bytes, stream);
+}
+
+extern "C" hipError_t deltanet_chunk_prefill_norm_fused(
+    const void* q, const void* k, const void* v, const float* g, const float* beta, const void* z,
+    const void* norm_weight, float eps, void* y, const float* initial_state, float* final_state,
+    int B, int T, int HV, int HQK, int DK, int DV, int chunk_size, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+    if (!norm_args_ok(q, k, v, g, beta, z, norm_weight, eps, y, final_state, B, T, HV, HQK, DK,
+                      DV, chunk_size, workspace))
+        return hipErrorInvalidValue;
     // The epilogue's groups wait on each other (the 8 slice groups of a head
-    // share every row's sum of squares), so it runs only when the whole scan
-    // grid is resident at once; otherwise the prefill writes o into y and the
-    // gated RMSNorm kernel rewrites it in place.
-    const long long groups = (long long)((B * HV + 7) / 8) * 8 * kSlicesPerHead;
-    const int cus = device_cus();
+    // share every row's sum of squares): it runs only when the runtime's
+    // occupancy figure says the whole scan grid fits at once, and then as a
+    // cooperative launch, which the runtime starts only with every group
+    // resident.  Otherwise the two-kernel path runs.
+    if (!norm_scan_coresident(scan_groups(B, HV)))
+        return prefill_then_norm(q, k, v, g, beta, z, norm_weight, eps, y, initial_state,
+                                 final_state, B, T, HV, HQK, workspace, workspace_bytes, stream);
+    const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);
     const NormIn n{static_cast<const uint16_t*>(z), static_cast<const uint16_t*>(norm_weight), eps};
-    if (cus > 0 && groups <= cus)
-        return launch_prefill(plain_in(q, k, v, g, beta), 0, y, initial_state, final_state,
-                              nullptr, B, T, B * T, HV, HQK, nc, workspace, workspace_bytes,
-                              stream, 0, nullptr, -1, kDefaultSpin, &n);
-    hipError_t e = launch_prefill(plain_in(q, k, v, g, beta), 0, y, initial_state, final_state,
-                                  nullptr, B, T, B * T, HV, HQK, nc, workspace, workspace_bytes,
-                                  stream, 0);
-    if (e != hipSuccess || T == 0) return e;
-    return gdn_gated_rmsnorm_forward(y, z, norm_weight, y, (int64_t)B * T * HV, kDV, eps,
-                                     GDN_DTYPE_BF16, GDN_DTYPE_BF16, stream);
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, y, initial_state, final_state, nullptr,
+                          B, T, B * T, HV, HQK, nc, workspace, workspace_bytes, stream, 0, nullptr,
+                          -1, kDefaultSpin, &n);
 }
 
 extern "C" hipError_t deltanet_prefill_status(const void* workspace, size_t workspace_bytes,
@@ -2112,6 +2160,73 @@ extern "C" int deltanet_varlen_chunk_map(const int32_t* cu_seqlens, int num_seqs
     return bound;
 }
 
+// Host twins of the kernels' block-cooperative lookups: the same phases, run
+// for every simulated thread between the points where the kernel has a
+// barrier, on the shared gdn_seq.h arithmetic.
+extern "C" int deltanet_varlen_chunks_before(const int32_t* cu_seqlens, int num_seqs,
+                                             int total_tokens, int upto, int nt) {
+    if (!cu_seqlens || num_seqs <= 0 || total_tokens < 0 || upto < 0 || upto > num_seqs ||
+        nt < 64 || nt > 1024 || nt % 64 != 0)
+        return -1;
+    std::vector<int> acc(nt, 0), nxt(nt);
+    for (int t = 0; t < nt; ++t)
+        for (int s = t; s < upto; s += nt)
+            acc[t] = sat_add(acc[t], seq_chunks(cu_seqlens, 0, total_tokens, s));
+    for (int off = 32; off > 0; off >>= 1) {   // butterfly within each wave of 64
+        for (int t = 0; t < nt; ++t) nxt[t] = sat_add(acc[t], acc[t ^ off]);
+        acc.swap(nxt);
+    }
+    int tot = 0;
+    for (int w = 0; w < nt / 64; ++w) tot = sat_add(tot, acc[w * 64]);
+    return tot;
+}
+
+extern "C" int deltanet_varlen_locate_chunk(const int32_t* cu_seqlens, int num_seqs,
+                                            int total_tokens, int cid, int nt,
+                                            int32_t* seq_tok_rows) {
+    if (!cu_seqlens || !seq_tok_rows || num_seqs <= 0 || total_tokens < 0 || nt < 2 ||
+        nt > 1024 || (nt & (nt - 1)) != 0)
+        return -1;
+    const int N = num_seqs;
+    std::vector<int> red(nt), cnt(nt), incl(nt), v(nt);
+    int base = 0;
+    bool found = false;
+    for (int s0 = 0; s0 < N && base < kSatChunks; s0 += nt) {
+        for (int t = 0; t < nt; ++t) {
+            const int s = s0 + t;
+            cnt[t] = (s < N) ? seq_chunks(cu_seqlens, 0, total_tokens, s) : 0;
+            red[t] = cnt[t];
+        }
+        for (int off = 1; off < nt; off <<= 1) {
+            for (int t = 0; t < nt; ++t) v[t] = scan_step(red.data(), t, off);
+            red.swap(v);
+        }
+        for (int t = 0; t < nt; ++t) incl[t] = red[t];
+        const int blk = red[nt - 1];
+        red[0] = -1;
+        red[1] = -1;
+        for (int t = 0; t < nt; ++t) {
+            if (owns_chunk(cnt[t], incl[t], base, cid)) {
+                red[0] = s0 + t;
+                red[1] = cid - base - (incl[t] - cnt[t]);
+            }
+        }
+        const bool here = cid < sat_add(base, blk);
+        if (here) {
+            int tok0 = 0, rows = 0;
+            found = seq_chunk_rows(cu_seqlens, N, 0, total_tokens, red[0], red[1], tok0, rows);
+            if (found) {
+                seq_tok_rows[0] = red[0];
+                seq_tok_rows[1] = tok0;
+                seq_tok_rows[2] = rows;
+            }
+        }
+        base = sat_add(base, blk);
+        if (here) break;
+    }
+    return found ? 1 : 0;
+}
+
 // Twins of the reference's bf16-wmma o-pass variant (kernels/chunk_delta_cuda_tco.h);
 // one implementation serves both names.
 extern "C" size_t deltanet_tcop_prefill_workspace_size(int B, int T, int HV, int DK, int DV,
@@ -2230,4 +2345,11 @@ extern "C" hipError_t deltanet_chunk_prefill_noalloc(const void* q, const void* 
     if (e != hipSuccess) return e;
     return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
                           T, B * T, HV, HQK, nc, ws, kNoAllocScratchBytes, stream, 0);
+}
+
+extern "C" hipError_t deltanet_prefill_noalloc_status(hipStream_t stream) {
+    void* ws = nullptr;
+    const hipError_t e = noalloc_scratch(&ws);
+    if (e != hipSuccess) return e;
+    return deltanet_prefill_status(ws, kNoAllocScratchBytes, stream);
 }

@@ -51,4 +51,44 @@ GDN_HD inline int seq_chunks_bounded(const int32_t* cu, int T, int total, int s,
     return room <= 0 ? 0 : (n < room ? n : room);
 }
 
+// Prefix sums of chunk counts saturate at kSatChunks, far above any chunk
+// bound a workspace can hold, so even adversarial cu_seqlens cannot wrap
+// them.  For a, b >= 0, sat_add(a, b) = min(a + b, kSatChunks), which is
+// associative and commutative: every reduction order gives the same sum.
+constexpr int kSatChunks = 1 << 30;
+
+GDN_HD inline int sat_add(int a, int b) {
+    const long long s = (long long)a + b;
+    return s > kSatChunks ? kSatChunks : (int)s;
+}
+
+// Step `off` of the block-cooperative inclusive scan (Hillis-Steele) over
+// red[0, NT): thread tid's new value.
+GDN_HD inline int scan_step(const int* red, int tid, int off) {
+    return tid >= off ? sat_add(red[tid], red[tid - off]) : red[tid];
+}
+
+// Whether the sequence holding `cnt` chunks, whose inclusive prefix within a
+// block of sequences is `incl` and whose block starts at chunk id `base`,
+// holds chunk id cid (exact while the prefix has not saturated).
+GDN_HD inline bool owns_chunk(int cnt, int incl, int base, int cid) {
+    const int excl = incl - cnt;
+    return cnt > 0 && incl < kSatChunks && cid >= base + excl && cid < base + incl;
+}
+
+// Chunk c of sequence seq (0 <= seq < N): its first token and row count, or
+// false when no such chunk exists.  Whatever seq and c a lookup produced,
+// a true result names rows [tok0, tok0 + rows) inside [0, total), 1 <= rows
+// <= 64.
+GDN_HD inline bool seq_chunk_rows(const int32_t* cu, int N, int T, int total, int seq, int c,
+                                  int& tok0, int& rows) {
+    if (seq < 0 || seq >= N || c < 0) return false;
+    const int n = seq_count(cu, T, total, seq);
+    if (c >= n / kChunkRows + (n % kChunkRows != 0)) return false;
+    tok0 = seq_lo(cu, T, total, seq) + c * kChunkRows;
+    const int left = n - c * kChunkRows;
+    rows = left < kChunkRows ? left : kChunkRows;
+    return true;
+}
+
 }  // namespace gdn

@@ -9,10 +9,11 @@
 // libgdn_hip.so (include/gdn_hip.h) with raw pointers; no torch types cross
 // that boundary.  New relative to the reference: a trailing keyword
 // `cu_seqlens` (varlen prefill), `recurrent_step` (decode),
-// `gated_rmsnorm`, `chunk_prefill_norm` (prefill with the gated RMSNorm in its
-// output stage), `chunk_prefill_fused` (the TensorRT adapter's whole GDN
-// step on raw inputs) and the causal conv1d ops `causal_conv1d_fwd` /
-// `causal_conv1d_update` that produce q/k/v upstream of the recurrence.
+// `gated_rmsnorm`, `chunk_prefill_norm` (prefill followed by the gated
+// RMSNorm, optionally fused into the scan's output stage),
+// `chunk_prefill_fused` (the TensorRT adapter's whole GDN step on raw inputs)
+// and the causal conv1d ops `causal_conv1d_fwd` / `causal_conv1d_update` that
+// produce q/k/v upstream of the recurrence.
 #include <torch/extension.h>
 
 // ROCm torch reports HIP devices as DeviceType::CUDA; the *MasqueradingAsCUDA
@@ -199,13 +200,14 @@ std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tens
     return chunk_prefill_impl(q, k, v, g, beta, s0, cu_seqlens, /*debug=*/true);
 }
 
-// Prefill with the gated RMSNorm fused into its output stage: returns
-// [y, final_state], y = gated_rmsnorm(o, z, weight, eps) for the o that
-// chunk_prefill would return (bf16 o, z and weight).
+// Prefill followed by the gated RMSNorm: returns [y, final_state], y =
+// gated_rmsnorm(o, z, weight, eps) for the o that chunk_prefill would return
+// (bf16 o, z and weight).  fused=True runs the RMSNorm in the scan's output
+// stage (deltanet_chunk_prefill_norm_fused), so o is never stored.
 std::vector<at::Tensor> chunk_prefill_norm(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
                                            at::Tensor beta, at::Tensor z, at::Tensor weight,
                                            std::optional<at::Tensor> s0, double eps,
-                                           bool checked) {
+                                           bool checked, bool fused) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && g.is_cuda() && beta.is_cuda() &&
                     z.is_cuda() && weight.is_cuda(),
                 "all inputs must be CUDA tensors");
@@ -251,12 +253,11 @@ std::vector<at::Tensor> chunk_prefill_norm(at::Tensor q, at::Tensor k, at::Tenso
                                                                  (int)DV, kChunk);
     TORCH_CHECK(ws_bytes > 0, "unsupported prefill configuration");
     auto ws = at::empty({(int64_t)ws_bytes}, vc.options().dtype(at::kByte));
-    check_hip(deltanet_chunk_prefill_norm(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                          gc.data_ptr<float>(), bc.data_ptr<float>(),
-                                          zc.data_ptr(), wc.data_ptr(), (float)eps, y.data_ptr(),
-                                          s0p, sf.data_ptr<float>(), (int)B, (int)T, (int)HV,
-                                          (int)HQK, (int)DK, (int)DV, kChunk, ws.data_ptr(),
-                                          ws_bytes, current_stream()),
+    auto entry = fused ? deltanet_chunk_prefill_norm_fused : deltanet_chunk_prefill_norm;
+    check_hip(entry(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr<float>(),
+                    bc.data_ptr<float>(), zc.data_ptr(), wc.data_ptr(), (float)eps, y.data_ptr(),
+                    s0p, sf.data_ptr<float>(), (int)B, (int)T, (int)HV, (int)HQK, (int)DK,
+                    (int)DV, kChunk, ws.data_ptr(), ws_bytes, current_stream()),
               "deltanet_chunk_prefill_norm");
     if (checked)
         check_hip(deltanet_prefill_status(ws.data_ptr(), ws_bytes, current_stream()),
@@ -474,10 +475,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "s0"_a = std::nullopt, pybind11::kw_only(),
           "cu_seqlens"_a = std::nullopt);
     m.def("chunk_prefill_norm", &chunk_prefill_norm,
-          "prefill with the gated RMSNorm fused into its output stage; returns [y, final_state], "
-          "y = gated_rmsnorm(o, z, weight, eps) for chunk_prefill's o",
+          "prefill followed by the gated RMSNorm; returns [y, final_state], y = "
+          "gated_rmsnorm(o, z, weight, eps) for chunk_prefill's o; fused=True runs the norm in "
+          "the scan's output stage",
           "q"_a, "k"_a, "v"_a, "g"_a, "beta"_a, "z"_a, "weight"_a, "s0"_a = std::nullopt,
-          pybind11::kw_only(), "eps"_a = 1e-6, "checked"_a = false);
+          pybind11::kw_only(), "eps"_a = 1e-6, "checked"_a = false, "fused"_a = false);
     m.def("_chunk_prefill_spin_limit", &chunk_prefill_spin_limit,
           "test entry: prefill with the scan's bounded waits limited to `spin` polls; returns "
           "[o, final_state, status]",

@@ -8,12 +8,13 @@ The compiled pieces live next to this file:
 
 ``load()`` returns the extension module, whose ops are
 
-  chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False)
-                                                       -> [o, final_state]
-  chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g]
+  chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False,
+                checked=False)                         -> [o, final_state]
+  chunk_prefill_debug(...)  -> [o, final_state, T, A, cumsum_g, T_post_leaf, M, S_chunk]
   recurrent_step(q, k, v, g, beta, state, *, qk_l2norm=False) -> o
                                                         (state updated in place)
-  chunk_prefill_norm(q, k, v, g, beta, z, weight, s0=None, *, eps=1e-6, checked=False)
+  chunk_prefill_norm(q, k, v, g, beta, z, weight, s0=None, *, eps=1e-6, checked=False,
+                     fused=False)
                           -> [gated_rmsnorm(o, z, weight), final_state]
   chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state) -> o
                           raw q/k/v and gate inputs     (state updated in place)
@@ -21,6 +22,10 @@ The compiled pieces live next to this file:
   causal_conv1d_fwd(x, weight, bias=None, silu=False) -> y      x, y [B, D, T]
   causal_conv1d_update(x, conv_state, weight, bias=None, silu=False) -> y
                                                   (conv_state updated in place)
+
+``checked=True`` synchronises after the call and raises when one of the
+scan's bounded waits gave up (o and the state would then be incomplete);
+the default leaves the call asynchronous.
 
 There is no fallback: if the extension is not built, ``load()`` raises.
 Build with ``python qwen-drive-edge-orin_amd/build.py``.
@@ -55,16 +60,20 @@ def load():
     return _mod
 
 
-def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False):
-    return load().chunk_prefill(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens, qk_l2norm=qk_l2norm)
+def chunk_prefill(q, k, v, g, beta, s0=None, *, cu_seqlens=None, qk_l2norm=False,
+                  checked=False):
+    return load().chunk_prefill(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens, qk_l2norm=qk_l2norm,
+                                checked=checked)
 
 
 def chunk_prefill_debug(q, k, v, g, beta, s0=None, *, cu_seqlens=None):
     return load().chunk_prefill_debug(q, k, v, g, beta, s0, cu_seqlens=cu_seqlens)
 
 
-def chunk_prefill_norm(q, k, v, g, beta, z, weight, s0=None, eps=1e-6):
-    return load().chunk_prefill_norm(q, k, v, g, beta, z, weight, s0, eps=eps)
+def chunk_prefill_norm(q, k, v, g, beta, z, weight, s0=None, *, eps=1e-6, checked=False,
+                       fused=False):
+    return load().chunk_prefill_norm(q, k, v, g, beta, z, weight, s0, eps=eps, checked=checked,
+                                     fused=fused)
 
 
 def chunk_prefill_fused(q, k, v, a, b, A_log, dt_bias, state):

@@ -35,14 +35,20 @@ _PROTOS = {
     "deltanet_prefill_live_workspace_size": (c_size_t, [c_int] * 6),
     "deltanet_chunk_prefill_norm": (hipError_t, [vp, vp, vp, fp, fp, vp, vp, c_float, vp, fp, fp] +
                                     [c_int] * 7 + [vp, c_size_t, hipStream_t]),
+    "deltanet_chunk_prefill_norm_fused": (hipError_t, [vp, vp, vp, fp, fp, vp, vp, c_float, vp,
+                                                       fp, fp] + [c_int] * 7 +
+                                          [vp, c_size_t, hipStream_t]),
     "deltanet_chunk_prefill_noalloc": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] +
                                        [c_int] * 7 + [hipStream_t]),
+    "deltanet_prefill_noalloc_status": (hipError_t, [hipStream_t]),
     "deltanet_prefill_varlen_workspace_size": (c_size_t, [c_int] * 6),
     "deltanet_prefill_varlen_live_workspace_size": (c_size_t, [c_int] * 6),
     "deltanet_prefill_status": (hipError_t, [vp, c_size_t, hipStream_t]),
     "deltanet_chunk_prefill_spin": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 4 +
                                     [vp, c_size_t, hipStream_t, ct.c_uint]),
     "deltanet_varlen_chunk_map": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
+    "deltanet_varlen_chunks_before": (c_int, [vp, c_int, c_int, c_int, c_int]),
+    "deltanet_varlen_locate_chunk": (c_int, [vp, c_int, c_int, c_int, c_int, vp]),
     "deltanet_chunk_prefill_varlen": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, i32p] +
                                       [c_int] * 7 + [vp, c_size_t, hipStream_t, c_int]),
     "deltanet_recurrent_step": (hipError_t, [vp, vp, vp, fp, fp, vp, fp] + [c_int] * 6 +

@@ -13,10 +13,18 @@ bf16 q/k/v and fp32 g/beta/state and return bf16 outputs.
 Only what the kernels implement is accepted: head dims of 128, any scale (q
 is rescaled), l2-normalised or raw q/k.  Anything else raises; there is no
 silent fallback to another implementation.
+
+The prefill's scan waits on its own stages with bounded waits; one that gives
+up (another process holding the device for ~0.1 s, say) leaves o and the
+state incomplete and sets a status word.  With the environment variable
+``GDN_HIP_CHECKED=1`` set when this module is imported, every prefill call
+synchronises and raises ``RuntimeError`` on such a give-up (a debug mode:
+the check costs a host synchronisation per call).
 """
 from __future__ import annotations
 
 import math
+import os
 import sys
 from pathlib import Path
 
@@ -28,6 +36,7 @@ import gdn_hip  # noqa: E402
 
 _D = 128
 _KERNEL_SCALE = 1.0 / math.sqrt(_D)
+_CHECKED = os.environ.get("GDN_HIP_CHECKED", "0") not in ("", "0")
 
 
 def _l2norm(x, eps=1e-6):
@@ -91,9 +100,9 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
             raise ValueError("with cu_seqlens the batch must be one packed row (B = 1)")
         o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0,
                                       cu_seqlens=cu_seqlens.to(torch.int32).contiguous(),
-                                      qk_l2norm=norm)
+                                      qk_l2norm=norm, checked=_CHECKED)
     else:
-        o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0, qk_l2norm=norm)
+        o, sf = gdn_hip.chunk_prefill(q, k, v, g, beta, s0, qk_l2norm=norm, checked=_CHECKED)
     return o.to(out_dtype), (sf if output_final_state else None)
 
 

@@ -73,3 +73,34 @@ def test_rejects_host_tensors():
         m.chunk_gated_delta_rule(q, q, v, g, g)
     with pytest.raises(RuntimeError, match="HIP device"):
         m.recurrent_gated_delta_rule(q, q, v, g, g)
+
+
+@pytest.mark.parametrize("env,expect", [(None, False), ("0", False), ("1", True)])
+def test_checked_mode_reaches_the_op(monkeypatch, env, expect):
+    """GDN_HIP_CHECKED=1 at import makes every prefill call ask the op to check
+    the scan's status word (checked=True: synchronise and raise on a bounded
+    wait that gave up); unset or 0 leaves the call asynchronous.  The op and
+    the device-side conversions are stubbed: this checks the plumbing only."""
+    import torch
+
+    if env is None:
+        monkeypatch.delenv("GDN_HIP_CHECKED", raising=False)
+    else:
+        monkeypatch.setenv("GDN_HIP_CHECKED", env)
+    m = _adapter()
+    assert m._CHECKED is expect
+    seen = {}
+
+    def fake_prefill(q, k, v, g, beta, s0, **kw):
+        seen.update(kw)
+        return torch.zeros_like(v), None
+
+    monkeypatch.setattr(m, "_prepare", lambda q, k, v, g, beta, *a, **kw: (q, k, v, g, beta, 2,
+                                                                            False))
+    monkeypatch.setattr(m.gdn_hip, "chunk_prefill", fake_prefill)
+    x = torch.zeros(1, 4, 2, 128)
+    g = torch.zeros(1, 4, 2)
+    m.chunk_gated_delta_rule(x, x, x, g, g)
+    assert seen["checked"] is expect
+    m.chunk_gated_delta_rule(x, x, x, g, g, cu_seqlens=torch.tensor([0, 4]))
+    assert seen["checked"] is expect

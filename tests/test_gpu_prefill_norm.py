@@ -1,10 +1,12 @@
-"""Prefill with the gated RMSNorm fused into its output stage
-(deltanet_chunk_prefill_norm, torch op chunk_prefill_norm) against the two
-separate steps it replaces (chunk_prefill, then gated_rmsnorm) and against the
-oracle (fp64 prefill, then the oracle's gated RMSNorm with the transformers
-rounding steps, modeling_qwen3_5.py:175-184).
+"""Prefill followed by the gated RMSNorm (deltanet_chunk_prefill_norm, torch
+op chunk_prefill_norm) and its fused form with the norm in the scan's output
+stage (deltanet_chunk_prefill_norm_fused, chunk_prefill_norm(fused=True))
+against the two separate steps they replace (chunk_prefill, then
+gated_rmsnorm) and against the oracle (fp64 prefill, then the oracle's gated
+RMSNorm with the transformers rounding steps, modeling_qwen3_5.py:175-184).
 
-The fused path sums each row's squares over the eight 16-column slices in
+The default entry runs exactly those two kernels, so it is held bitwise.  The
+fused path sums each row's squares over the eight 16-column slices in
 another order than the standalone kernel, so a row's rsqrt can differ in its
 last bit and flip the bf16 rounding of n = o * rsqrt(...); that ulp of n
 passes through two more roundings (w * n, then * silu(z)).  The bar against
@@ -37,16 +39,31 @@ def _ulp_bf16(x):
     return torch.pow(2.0, e - 7)
 
 
+def test_prefill_norm_default_is_two_steps(ops, dev):
+    """The default entry is the prefill into y and the gated RMSNorm in place:
+    bitwise the two separate ops."""
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    z, w = _z_w(34, v.shape)
+    d = [t.to(dev) for t in (q, k, v, g, beta, s0, z, w)]
+    print("[prefill_norm] default entry T1141 HV32", flush=True)
+    y, sf = ops.chunk_prefill_norm(*d[:5], d[6], d[7], d[5], eps=1e-6, checked=True)
+    o2, sf2 = ops.chunk_prefill(*d[:6])
+    y2 = ops.gated_rmsnorm(o2, d[6], d[7], 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2) and torch.equal(sf, sf2)
+
+
 @pytest.mark.parametrize("B,T,HK,HV", [(1, 1141, 16, 32), (2, 100, 2, 4), (1, 64, 1, 1),
                                        (8, 70, 32, 64)])
-def test_prefill_norm_matches_two_steps(ops, dev, B, T, HK, HV):
-    """(8, 70, 32, 64) has 4096 scan groups, more than the chip's CUs: the
-    entry then takes the two-kernel path, which must give the same bits."""
+def test_prefill_norm_fused_matches_two_steps(ops, dev, B, T, HK, HV):
+    """(8, 70, 32, 64) has 4096 scan groups, more than fit the chip at once:
+    the fused entry then takes the two-kernel path, which must give the same
+    bits."""
     q, k, v, g, beta, s0 = gc.make_gdn_inputs(31, B, T, HK, HV, g_shift=2.0)
     z, w = _z_w(32, v.shape)
     d = [t.to(dev) for t in (q, k, v, g, beta, s0, z, w)]
-    print(f"[prefill_norm] B{B} T{T} HK{HK} HV{HV}", flush=True)
-    y, sf = ops.chunk_prefill_norm(*d[:5], d[6], d[7], d[5], eps=1e-6, checked=True)
+    print(f"[prefill_norm] fused B{B} T{T} HK{HK} HV{HV}", flush=True)
+    y, sf = ops.chunk_prefill_norm(*d[:5], d[6], d[7], d[5], eps=1e-6, checked=True, fused=True)
     o2, sf2 = ops.chunk_prefill(*d[:6])
     y2 = ops.gated_rmsnorm(o2, d[6], d[7], 1e-6)
     torch.cuda.synchronize()
@@ -60,9 +77,9 @@ def test_prefill_norm_matches_two_steps(ops, dev, B, T, HK, HV):
 
 
 def test_prefill_norm_matches_oracle(ops, dev):
-    """Two pins.  (1) The epilogue: y against the oracle's gated RMSNorm
-    applied to this build's own o (chunk_prefill's output, the same bits the
-    fused scan normalises), to the bar of the two-step test.  (2) End to end
+    """The fused path; two pins.  (1) The epilogue: y against the oracle's
+    gated RMSNorm applied to this build's own o (chunk_prefill's output, the
+    same bits the fused scan normalises), to the bar of the two-step test.  (2) End to end
     against the fp64 oracle: y = gated_rmsnorm(o) scales o's absolute error by
     |w silu(z)| / rms(o), so the bar is the reference harness's fixture bar on
     the whole tensor (L2-rel < 3e-3, cos >= 0.9999,
@@ -71,7 +88,7 @@ def test_prefill_norm_matches_oracle(ops, dev):
     q, k, v, g, beta, s0 = gc.prefill_inputs()
     z, w = _z_w(33, v.shape)
     d = [t.to(dev) for t in (q, k, v, g, beta, s0, z, w)]
-    y, sf = ops.chunk_prefill_norm(*d[:5], d[6], d[7], d[5], eps=1e-6, checked=True)
+    y, sf = ops.chunk_prefill_norm(*d[:5], d[6], d[7], d[5], eps=1e-6, checked=True, fused=True)
     o, _ = ops.chunk_prefill(*d[:6])
     torch.cuda.synchronize()
     yc = y.cpu()
@@ -103,6 +120,7 @@ def test_prefill_norm_capi_rejects(lib, dev):
     base = [p, p, p, p, p]
     for z, w, y, eps in [(None, p, p, 1e-6), (p, None, p, 1e-6), (p, p, None, 1e-6),
                          (p, p, p, -1.0)]:
-        err = lib.deltanet_chunk_prefill_norm(*base, z, w, eps, y, None, p, B, T, HV, HK, D, D,
-                                              64, ws.data_ptr(), wsb, None)
-        assert err == capi.HIP_ERROR_INVALID_VALUE
+        for entry in (lib.deltanet_chunk_prefill_norm, lib.deltanet_chunk_prefill_norm_fused):
+            err = entry(*base, z, w, eps, y, None, p, B, T, HV, HK, D, D, 64, ws.data_ptr(), wsb,
+                        None)
+            assert err == capi.HIP_ERROR_INVALID_VALUE

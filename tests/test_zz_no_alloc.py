@@ -1,8 +1,9 @@
 """deltanet_chunk_prefill_noalloc (the allocation-free prefill, whose
 workspace is a static device array) against deltanet_chunk_prefill with a
 caller workspace, through the C ABI: identical o and final state on two calls
-in a row, the second on a smaller input, and a host-side reject of a size the
-array cannot hold."""
+in a row, the second on a smaller input, a clear status word after each
+(deltanet_prefill_noalloc_status), and a host-side reject of a size the array
+cannot hold."""
 import pytest
 import torch
 
@@ -32,6 +33,8 @@ def _run_pair(lib, dev, seed, B, T, HK, HV):
     sf = torch.full_like(s0, float("nan"))
     assert lib.deltanet_chunk_prefill_noalloc(*args, o.data_ptr(), s0.data_ptr(), sf.data_ptr(),
                                               B, T, HV, HK, D, D, 64, _stream()) == capi.HIP_SUCCESS
+    # no bounded wait of the call gave up (the status word in the array's header)
+    assert lib.deltanet_prefill_noalloc_status(_stream()) == capi.HIP_SUCCESS
     torch.cuda.synchronize()
     assert torch.equal(o, o_ref), "o differs from the workspace entry"
     assert torch.equal(sf, s_ref), "final state differs from the workspace entry"
