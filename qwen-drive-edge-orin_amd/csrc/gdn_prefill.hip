@@ -920,6 +920,7 @@ struct ScanSmem {
                      // (V, gates of c + 1) have landed
     int uready;      // chunks whose U is in ring P (producer)
     int freeC;       // chunks whose ring-C and ring-P stages the chain has finished reading
+    int kfree;       // chunks whose ring-C K^T the lo helper has finished reading
     int ready;       // chunks whose hand-off slot the chain has written
     int cons[2];     // per output wave: chunks of its parity whose hand-off slot it has read
     int dvready;     // chunks whose d o V_n the chain has handed to the helper
@@ -1058,9 +1059,15 @@ __device__ void run_loader(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
         for (int c = 0; c < kLeadP; ++c) issue_p(c);
     }
     for (int c = j; c < x.nch; c += 2) {
-        // ring-C stage c % kRingC held chunk c - kRingC; ring-P stage
-        // (c + kLeadP) % kRingP held chunk c + kLeadP - kRingP <= c - kRingC
-        if (!w.until([&] { return lds_ld(&sm.freeC) >= c - kRingC + 1; })) break;
+        // ring-C stage c % kRingC held chunk c - kRingC (read by the chain
+        // and the lo helper); ring-P stage (c + kLeadP) % kRingP held chunk
+        // c + kLeadP - kRingP <= c - kRingC
+        if (!w.until([&] {
+                const bool fc = lds_ld(&sm.freeC) >= c - kRingC + 1;
+                const bool fk = lds_ld(&sm.kfree) >= c - kRingC + 1;
+                return fc & fk;
+            }))
+            break;
         asm volatile("" ::: "memory");
         issue_c(c);
         asm volatile("" ::: "memory");   // ring P's loads are issued after ring C's
@@ -1370,6 +1377,7 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
             lds_st(&sm.ready, c + 1);
             lds_st(&sm.freeC, c + 1);
             if (!kDbg) lds_st(&sm.dvready, c + 1);
+            else lds_st(&sm.kfree, c + 1);   // no helper: the chain read K^T
         }
     }
     if (!ok) return;
@@ -1391,33 +1399,32 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
 // Lo helper (SIMD 3): Sc <- e^{c63} Sc + K^T lo per chunk, with d o V_n from
 // the chain split again into its bf16 hi part and the residual lo =
 // bf16(d o V_n - hi), the same values the chain's hi part leaves out.  The K^T
-// fragments come straight from global memory (the loaders have just brought
-// them into L2), two chunks ahead in two register sets used in turn, so ring
-// C never waits for this wave.  After
-// the last chunk Sc goes to the lo slots for the chain.
+// fragments are read from the chunk's ring-C stage, which the loaders refill
+// only after this wave has read it (kfree): each chunk's K^T crosses from L2
+// to the CU once.  After the last chunk Sc goes to the lo slots for the chain.
 __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                               int lane) {
     if (x.nch <= 0) return;
     f32x4 Sc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) Sc[t] = zero4();
-    auto load_kt = [&](int c, u32x4 (&k)[16]) {
-        const int cc = min(c, x.nch - 1);
-        const u32x4* src = a.ws.KT + ((size_t)(x.chunk0 + cc) * a.HK + x.hk) * (16 * 64) + lane;
-#pragma unroll
-        for (int f = 0; f < 16; ++f) k[f] = src[f * 64];
-    };
-    // one chunk with K^T in kc; then chunk c + 2's K^T goes into kc
-    auto step = [&](int c, u32x4 (&kc)[16]) -> bool {
-        if (!w.until([&] { return lds_ld(&sm.dvready) >= c + 1; })) return false;
+    for (int c = 0; c < x.nch; ++c) {
+        if (!w.until([&] { return lds_ld(&sm.dvready) >= c + 1; })) return;
         asm volatile("" ::: "memory");
         const LoHand& lh = sm.lo[c % kLoSlots];
+        const StageC& sc = sm.c[c % kRingC];
         f32x4 d[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) d[mt] = lh.d[mt][lane];
         const float gam = lh.gam;
+        u32x4 kc[16];
+#pragma unroll
+        for (int f = 0; f < 16; ++f) kc[f] = sc.KT[f][lane];
         lds_wait_all();
-        if (lane == 0) lds_st(&sm.lodone, c + 1);
+        if (lane == 0) {
+            lds_st(&sm.lodone, c + 1);
+            lds_st(&sm.kfree, c + 1);
+        }
         bf16x8 lo[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -1443,16 +1450,6 @@ __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, 
             for (int t = 0; t < 8; ++t)
                 Sc[t] = mfma16_bf16(__builtin_bit_cast(bf16x8, kc[t * 2 + kb]), lo[kb], Sc[t]);
         }
-        load_kt(c + 2, kc);
-        return true;
-    };
-    u32x4 k0[16], k1[16];
-    load_kt(0, k0);
-    load_kt(1, k1);
-    // step() is false only when a bounded wait gave up
-    for (int c = 0; c < x.nch; c += 2) {
-        if (!step(c, k0)) return;
-        if (c + 1 < x.nch && !step(c + 1, k1)) return;
     }
     // every chunk's slot has been read: Sc goes to the lo slots
     f32x4* dst = &sm.lo[0].d[0][0];
@@ -1763,6 +1760,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
         lds_st(&sm.pfill[1], 0);
         lds_st(&sm.uready, 0);
         lds_st(&sm.freeC, 0);
+        lds_st(&sm.kfree, 0);
         lds_st(&sm.ready, 0);
         lds_st(&sm.cons[0], 0);
         lds_st(&sm.cons[1], 0);
