@@ -84,8 +84,11 @@ int deltanet_varlen_locate_chunk(const int32_t* cu_seqlens, int num_seqs, int to
 /* HBM streaming probe (benchmarks only): kind 0 reads a and b and writes
  * c = a ^ b, `bytes` each (three streams, the gated RMSNorm's pattern);
  * kind 1 reads and rewrites c in place (the decode state's pattern).
- * nontemporal != 0 uses non-temporal loads and stores.  `blocks` work-groups
- * of 256 threads stride over the 16-byte vectors.  bytes must be a nonzero
+ * nontemporal != 0 uses non-temporal loads and stores.  For kinds 0 and 1
+ * `blocks` work-groups of 256 threads stride over the 16-byte vectors.  Kind
+ * 2 is kind 0 in the gated RMSNorm's own launch shape, one pass with no loop:
+ * each of the 256 threads of ceil(bytes / (4096 P)) work-groups moves
+ * P = `blocks` (1..4) vectors, 256 vectors apart.  bytes must be a nonzero
  * multiple of 16, otherwise hipErrorInvalidValue. */
 hipError_t gdn_stream_probe(int kind, int nontemporal, const void* a, const void* b, void* c,
                             size_t bytes, int blocks, hipStream_t stream);

@@ -230,3 +230,16 @@ def test_reference_module_names_import():
     for name in ("deltanet_chunk_cuda", "deltanet_chunk_cuda_tco"):
         mod = importlib.import_module(name)
         assert callable(mod.chunk_prefill) and callable(mod.chunk_prefill_debug), name
+
+
+def test_stream_probe_rejects_on_host(lib):
+    """gdn_stream_probe's host checks: unknown kind, size not a multiple of
+    16, missing buffers, and more than 4 pieces per lane for the one-pass
+    kind 2."""
+    p = 16
+    assert lib.gdn_stream_probe(3, 0, p, p, p, 1024, 4, None) == INVALID
+    assert lib.gdn_stream_probe(0, 0, p, p, p, 1000, 4, None) == INVALID
+    assert lib.gdn_stream_probe(0, 0, None, p, p, 1024, 4, None) == INVALID
+    assert lib.gdn_stream_probe(2, 1, p, None, p, 1024, 1, None) == INVALID
+    assert lib.gdn_stream_probe(2, 1, p, p, p, 1024, 5, None) == INVALID
+    assert lib.gdn_stream_probe(1, 0, None, None, None, 1024, 4, None) == INVALID
