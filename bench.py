@@ -314,6 +314,80 @@ def bench_hf_lane(ops, dev, steps, warmup):
     return dict(ms_k=ms_k, ms_t=ms_t)
 
 
+def bench_twolevel(ops, dev, reps=10):
+    """The two-level chunk-group scan prototype (deltanet_chunk_prefill_twolevel)
+    against the plain call on the same warm inputs: the T=1141 HV=32 layer and
+    the 8-sequence packed batch at 4 segments per sequence, and one long
+    sequence with few heads (B=1 T=16384 HV=4 HK=2) at 8 segments, where the
+    plain scan leaves most CUs idle.  Device time from the call's own events
+    (median of `reps`), split into prep, pass 1 (B), pass 1 (Phi), combine and
+    replay; the serial chain depth (chunks a scan walks in a row) of each."""
+    import ctypes as ct
+    import torch
+    import gdn_cases as gc
+    from gdn_hip import capi
+
+    lib = capi.lib()
+    hip = _Hip()
+    stream = torch.cuda.current_stream().cuda_stream
+    cases = []
+    q, k, v, g, beta, s0 = gc.prefill_inputs()
+    cases.append(("T1141_HV32_4seg", (q, k, v, g, beta, s0), None, 4))
+    vq, vk, vv, vg, vb, vs0, cu = gc.varlen_inputs()
+    cases.append(("varlen_8seq_4seg", (vq, vk, vv, vg, vb, vs0), cu, 4))
+    lq, lk, lv, lg, lb, ls0 = gc.make_gdn_inputs(12, B=1, T=16384, HK=2, HV=4, g_shift=2.0)
+    cases.append(("T16384_HV4_8seg", (lq, lk, lv, lg, lb, ls0), None, 8))
+    out = {}
+    for name, ten, cu_t, segs in cases:
+        d = [t.to(dev) for t in ten]
+        if cu_t is None:
+            N, T = d[0].shape[0], d[0].shape[1]
+            cu_p = None
+            lens = [T] * N
+        else:
+            N, T = len(cu_t) - 1, int(cu_t[-1])
+            cu_h = (ct.c_int32 * len(cu_t))(*[int(x) for x in cu_t])
+            cu_p = ct.cast(cu_h, ct.c_void_p)
+            lens = [int(cu_t[i + 1] - cu_t[i]) for i in range(N)]
+        HV, HK = d[2].shape[2], d[0].shape[2]
+        o = torch.empty_like(d[2])
+        sf = torch.empty(N, HV, 128, 128, device=dev)
+        wsb = lib.deltanet_prefill_twolevel_workspace_size(cu_p, N, T, HV, segs)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        evs = hip.events(6)
+        parts = []
+        for r in range(reps + 2):
+            err = lib.deltanet_chunk_prefill_twolevel(
+                *[t.data_ptr() for t in d[:5]], o.data_ptr(), d[5].data_ptr(), sf.data_ptr(),
+                cu_p, N, T, HV, HK, segs, ws.data_ptr(), wsb, stream, evs, 6)
+            assert err == 0, err
+            torch.cuda.synchronize()
+            if r >= 2:
+                parts.append([hip.elapsed_ms(evs[i], evs[i + 1]) * 1e3 for i in range(5)])
+        hip.destroy(evs)
+        med = [sorted(p[i] for p in parts)[len(parts) // 2] for i in range(5)]
+        if cu_t is None:
+            plain = lambda i: ops.chunk_prefill(*d)  # noqa: E731
+        else:
+            cud = cu_t.to(dev)
+            plain = lambda i: ops.chunk_prefill(*d, cu_seqlens=cud)  # noqa: E731
+        ms_plain = time_calls(plain, 1, reps * 2, 3)
+        nch = [(n + 63) // 64 for n in lens]
+        seg_len = max(-(-c // min(segs, c)) if c else 0 for c in nch)
+        out[name] = {"us_plain": round(ms_plain * 1e3, 2),
+                     "us_twolevel": round(sum(med), 2),
+                     "us_prep": round(med[0], 2), "us_pass1_B": round(med[1], 2),
+                     "us_pass1_Phi": round(med[2], 2), "us_combine": round(med[3], 2),
+                     "us_replay": round(med[4], 2),
+                     "serial_chunks_plain": max(nch),
+                     "serial_chunks_twolevel": 2 * seg_len + max(0, min(segs, max(nch)) - 2),
+                     "scan_groups_plain": -(-N * HV // 8) * 64,
+                     "scan_groups_per_pass_twolevel": -(-sum(min(segs, c) if c else 1
+                                                             for c in nch) * HV // 8) * 64}
+        del ws, d
+    return out
+
+
 def bench_conv(ops, dev, steps, warmup):
     """Causal conv1d + SiLU ahead of the recurrence: the prefill form over
     the layer's conv channels (D = 2 * 16 * 128 + 32 * 128 = 8192, T = 1141,
@@ -683,6 +757,7 @@ def main():
         pn = bench_prefill_norm(ops, dev, args.steps, args.warmup)
         hl = bench_hf_lane(ops, dev, args.steps, args.warmup)
         sp = bench_stream(dev, args.steps, args.warmup)
+        tl = bench_twolevel(ops, dev)
         line["secondary"] = {
             "gated_rmsnorm_1141x32x128": {
                 "us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
@@ -716,6 +791,7 @@ def main():
             "hf_lane_chunk_gated_delta_rule_T1141_HV32": {
                 "us": round(hl["ms_k"] * 1e3, 2),
                 "us_torch_l2norm_eager": round(hl["ms_t"] * 1e3, 2)},
+            "twolevel_scan_prototype": tl,
             "causal_conv1d_update_B64x8192_k4": {"us": round(cv["ms_d"] * 1e3, 2),
                                                  "GB/s": round(cv["gbs_d"], 1),
                                                  "hbm_frac": round(cv["frac_d"], 4)},

@@ -81,6 +81,29 @@ int deltanet_varlen_chunks_before(const int32_t* cu_seqlens, int num_seqs, int t
 int deltanet_varlen_locate_chunk(const int32_t* cu_seqlens, int num_seqs, int total_tokens,
                                  int cid, int nt, int32_t* seq_tok_rows);
 
+/* Two-level chunk-group scan (prototype for measurement; same results as
+ * deltanet_chunk_prefill / _varlen to rounding).  Each sequence's chunks are
+ * cut into `segments` chunk-aligned segments; pass 1 scans every segment
+ * from a zero state (end state B_j) and from the identity with v = 0 (the
+ * segment's transition Phi_j), a combine kernel forms the entry states
+ * E_j = Phi_{j-1} E_{j-1} + B_{j-1} in fp32, and a replay scans every segment
+ * from E_j.  cu_seqlens_host is HOST memory [num_seqs + 1] (well-formed,
+ * starting at 0), or NULL for num_seqs sequences of T tokens; T is the total
+ * token count when it is given.  The call synchronises `stream` once to copy
+ * its segment table.  events: NULL, or 6 events recorded at the start and
+ * after the prep, pass 1 (B), pass 1 (Phi), the combine and the replay.  No
+ * counterpart in the reference (its carry kernel is the plain serial scan,
+ * kernels/chunk_delta_cuda.cu:348-417). */
+size_t deltanet_prefill_twolevel_workspace_size(const int32_t* cu_seqlens_host, int num_seqs,
+                                                int T, int HV, int segments);
+hipError_t deltanet_chunk_prefill_twolevel(const void* q, const void* k, const void* v,
+                                           const float* g, const float* beta, void* o,
+                                           const float* initial_state, float* final_state,
+                                           const int32_t* cu_seqlens_host, int num_seqs, int T,
+                                           int HV, int HQK, int segments, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream,
+                                           hipEvent_t* events, int n_events);
+
 /* HBM streaming probe (benchmarks only): kind 0 reads a and b and writes
  * c = a ^ b, `bytes` each (three streams, the gated RMSNorm's pattern);
  * kind 1 reads and rewrites c in place (the decode state's pattern).

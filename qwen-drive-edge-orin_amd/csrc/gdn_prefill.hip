@@ -2351,3 +2351,257 @@ extern "C" hipError_t deltanet_prefill_noalloc_status(hipStream_t stream) {
     if (e != hipSuccess) return e;
     return deltanet_prefill_status(ws, kNoAllocScratchBytes, stream);
 }
+
+// ---------------------------------------------------------------------------
+// Two-level chunk-group scan (diagnostic): each sequence's chunks are cut
+// into `segments` chunk-aligned segments, which the kernels above treat as
+// sequences of their own (same global chunk ids, so one prep serves every
+// pass).  A chunk maps the state affinely, S -> A_n S + B_n, so a segment's
+// end state is Phi_j S_entry + B_j:
+//   pass 1a  scan from a zero state (the first segment of a sequence from its
+//            initial state): B_j, and the first segment's final outputs;
+//   pass 1b  scan of v = 0 from S = I: Phi_j = A_last ... A_first;
+//   combine  E_1 = (pass 1a end state of segment 0),
+//            E_j = Phi_{j-1} E_{j-1} + B_{j-1}, in fp32, serial over j;
+//   replay   scan from the entry states E_j: o and the final state.
+// The serial depth is max segment length (pass 1), segments - 2 (combine) and
+// max segment length (replay) instead of the sequence's chunk count, at
+// about three times the chain work.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kSt = kDK * kDV;   // floats per (sequence, head) state
+
+// s0a[seg] = the sequence's initial state for its first segment, else 0;
+// s0i[seg] = I; zero v rows.
+__global__ __launch_bounds__(256) void twolevel_init_kernel(const float* __restrict__ s0,
+                                                            const int32_t* __restrict__ seg_seq,
+                                                            const int32_t* __restrict__ seg_first,
+                                                            int nseg, int HV, float* s0a,
+                                                            float* s0i, uint32_t* zv,
+                                                            size_t zv_words) {
+    const size_t n = (size_t)nseg * HV * kSt;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t sh = i / kSt;
+        const int seg = (int)(sh / HV), h = (int)(sh % HV);
+        const int e = (int)(i % kSt), r = e / kDV, c = e % kDV;
+        const bool first = seg_first[seg] != 0;
+        s0a[i] = (first && s0) ? s0[((size_t)seg_seq[seg] * HV + h) * kSt + e] : 0.f;
+        s0i[i] = r == c ? 1.f : 0.f;
+    }
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < zv_words;
+         i += (size_t)gridDim.x * 256)
+        zv[i] = 0u;
+}
+
+// One work-group per (sequence, head, 16-column slice): the entry states of
+// the sequence's segments 1.. in order, E_j[:, slice] = Phi_{j-1} E_{j-1} +
+// B_{j-1} (fp32; E_1 = B_0, which already started from the initial state).
+__global__ __launch_bounds__(256) void twolevel_combine_kernel(
+    const float* __restrict__ phi, const float* __restrict__ bst,
+    const int32_t* __restrict__ seq_seg0, const int32_t* __restrict__ seq_nseg, int HV,
+    float* __restrict__ E) {
+    __shared__ float prev[kDK][16];
+    const int sl = blockIdx.x % 8, h = (blockIdx.x / 8) % HV, s = blockIdx.x / (8 * HV);
+    const int seg0 = seq_seg0[s], ns = seq_nseg[s];
+    const int t = threadIdx.x, r = t >> 1, c0 = (t & 1) * 8;
+    const int col = sl * 16 + c0;
+    if (ns < 2) return;
+    // E_1 = B_0
+    {
+        const float* b = bst + ((size_t)seg0 * HV + h) * kSt + (size_t)r * kDV + col;
+        float* e = E + ((size_t)(seg0 + 1) * HV + h) * kSt + (size_t)r * kDV + col;
+        for (int i = 0; i < 8; ++i) {
+            e[i] = b[i];
+            prev[r][c0 + i] = b[i];
+        }
+    }
+    __syncthreads();
+    for (int j = 2; j < ns; ++j) {
+        const float* p = phi + ((size_t)(seg0 + j - 1) * HV + h) * kSt + (size_t)r * kDV;
+        const float* b = bst + ((size_t)(seg0 + j - 1) * HV + h) * kSt + (size_t)r * kDV + col;
+        float acc[8];
+        for (int i = 0; i < 8; ++i) acc[i] = b[i];
+        for (int kk = 0; kk < kDK; ++kk) {
+            const float pv = p[kk];
+            for (int i = 0; i < 8; ++i) acc[i] = fmaf(pv, prev[kk][c0 + i], acc[i]);
+        }
+        __syncthreads();
+        float* e = E + ((size_t)(seg0 + j) * HV + h) * kSt + (size_t)r * kDV + col;
+        for (int i = 0; i < 8; ++i) {
+            e[i] = acc[i];
+            prev[r][c0 + i] = acc[i];
+        }
+        __syncthreads();
+    }
+}
+
+// final_state[s] = the replay's end state of sequence s's last segment
+__global__ __launch_bounds__(256) void twolevel_gather_kernel(const float* __restrict__ sfr,
+                                                              const int32_t* __restrict__ seq_last,
+                                                              int nseq, int HV,
+                                                              float* __restrict__ sf) {
+    const size_t n = (size_t)nseq * HV * kSt;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t sh = i / kSt;
+        const int s = (int)(sh / HV), h = (int)(sh % HV);
+        sf[i] = sfr[((size_t)seq_last[s] * HV + h) * kSt + i % kSt];
+    }
+}
+
+struct TwoLevelPlan {
+    std::vector<int32_t> seg_cu, seg_seq, seg_first, seq_seg0, seq_nseg, seq_last;
+    int nseg = 0, nseq = 0, total = 0, chunks = 0;
+};
+
+// Chunk-aligned segments of every sequence: sequence s of n_s chunks gets
+// min(segments, n_s) segments (one when it is empty) of near-equal chunk
+// counts.  cu_host NULL: B sequences of T tokens.
+bool twolevel_plan(const int32_t* cu_host, int nseq, int T, int segments, TwoLevelPlan& p) {
+    if (nseq <= 0 || segments <= 0 || segments > 1024) return false;
+    p.nseq = nseq;
+    p.seg_cu.assign(1, 0);
+    int pos = 0;
+    for (int s = 0; s < nseq; ++s) {
+        const int lo = cu_host ? cu_host[s] : s * T, hi = cu_host ? cu_host[s + 1] : (s + 1) * T;
+        if (lo != pos || hi < lo) return false;   // well-formed, starting at 0
+        const int len = hi - lo, nc = (len + kChunk - 1) / kChunk;
+        const int g = nc > 0 ? std::min(segments, nc) : 1;
+        p.seq_seg0.push_back(p.nseg);
+        p.seq_nseg.push_back(g);
+        for (int j = 0; j < g; ++j) {
+            const int c1 = (int)((long long)nc * (j + 1) / g);
+            p.seg_cu.push_back(j + 1 == g ? hi : lo + c1 * kChunk);
+            p.seg_seq.push_back(s);
+            p.seg_first.push_back(j == 0);
+        }
+        p.nseg += g;
+        p.seq_last.push_back(p.nseg - 1);
+        p.chunks += nc;
+        pos = hi;
+    }
+    p.total = pos;
+    return true;
+}
+
+size_t twolevel_ws_bytes(const TwoLevelPlan& p, int HV, size_t* off) {
+    size_t o = 0;
+    auto put = [&](int i, size_t bytes) {
+        off[i] = o;
+        o += align256(bytes);
+    };
+    const size_t st = (size_t)p.nseg * HV * kSt * 4;
+    put(0, WsLayout((size_t)std::max(p.chunks, 1) * HV).live);   // prefill workspace
+    put(1, (p.nseg + 1) * 4);                                      // seg cu
+    put(2, p.nseg * 4);                                            // seg -> sequence
+    put(3, p.nseg * 4);                                            // first-segment flags
+    put(4, p.nseq * 4 * 3);                                        // seq: first seg, count, last
+    for (int i = 5; i < 11; ++i) put(i, st);   // s0a, s0i, B, Phi, E, replay end states
+    put(11, (size_t)p.total * HV * kDV * 2);   // zero v
+    put(12, (size_t)p.total * HV * kDV * 2);   // pass 1b o (discarded)
+    return o;
+}
+
+}  // namespace
+
+extern "C" size_t deltanet_prefill_twolevel_workspace_size(const int32_t* cu_seqlens_host,
+                                                           int num_seqs, int T, int HV,
+                                                           int segments) {
+    TwoLevelPlan p;
+    if (HV <= 0 || T < 0 || !twolevel_plan(cu_seqlens_host, num_seqs, T, segments, p)) return 0;
+    size_t off[13];
+    return twolevel_ws_bytes(p, HV, off);
+}
+
+extern "C" hipError_t deltanet_chunk_prefill_twolevel(
+    const void* q, const void* k, const void* v, const float* g, const float* beta, void* o,
+    const float* initial_state, float* final_state, const int32_t* cu_seqlens_host, int num_seqs,
+    int T, int HV, int HQK, int segments, void* workspace, size_t workspace_bytes,
+    hipStream_t stream, hipEvent_t* events, int n_events) {
+    if (!dims_ok(HV, HQK, kDK, kDV, kChunk) || T < 0 || !final_state || !workspace)
+        return hipErrorInvalidValue;
+    if (events && n_events != 6) return hipErrorInvalidValue;
+    TwoLevelPlan p;
+    if (!twolevel_plan(cu_seqlens_host, num_seqs, T, segments, p)) return hipErrorInvalidValue;
+    if (p.total > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    size_t off[13];
+    if (workspace_bytes < twolevel_ws_bytes(p, HV, off)) return hipErrorInvalidValue;
+    char* base = static_cast<char*>(workspace);
+    auto at = [&](int i) { return base + off[i]; };
+    // the segment table, copied in (host memory: wait for the copy)
+    std::vector<int32_t> seqtab(p.seq_seg0);
+    seqtab.insert(seqtab.end(), p.seq_nseg.begin(), p.seq_nseg.end());
+    seqtab.insert(seqtab.end(), p.seq_last.begin(), p.seq_last.end());
+    hipError_t e = hipSuccess;
+    auto copy = [&](int i, const std::vector<int32_t>& h) {
+        if (e == hipSuccess && !h.empty())
+            e = hipMemcpyAsync(at(i), h.data(), h.size() * 4, hipMemcpyHostToDevice, stream);
+    };
+    copy(1, p.seg_cu);
+    copy(2, p.seg_seq);
+    copy(3, p.seg_first);
+    copy(4, seqtab);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return e;
+    const int32_t* seg_cu = reinterpret_cast<const int32_t*>(at(1));
+    const int32_t* seq_seg0 = reinterpret_cast<const int32_t*>(at(4));
+    float* s0a = reinterpret_cast<float*>(at(5));
+    float* s0i = reinterpret_cast<float*>(at(6));
+    float* bst = reinterpret_cast<float*>(at(7));
+    float* phi = reinterpret_cast<float*>(at(8));
+    float* E = reinterpret_cast<float*>(at(9));
+    float* sfr = reinterpret_cast<float*>(at(10));
+    void* zv = at(11);
+    void* o_junk = at(12);
+    void* ws = at(0);
+    const size_t wsb = off[1] - off[0];
+    const size_t nch = (size_t)std::max(p.chunks, 1);
+    auto rec = [&](int i) {
+        if (events) (void)hipEventRecord(events[i], stream);
+    };
+    rec(0);
+    const size_t zv_words = (size_t)p.total * HV * kDV / 2;
+    hipLaunchKernelGGL(twolevel_init_kernel, dim3(1024), dim3(256), 0, stream, initial_state,
+                       reinterpret_cast<const int32_t*>(at(2)),
+                       reinterpret_cast<const int32_t*>(at(3)), p.nseg, HV, s0a, s0i,
+                       static_cast<uint32_t*>(zv), zv_words);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const PrepIn in = plain_in(q, k, v, g, beta);
+    // prep over the segment chunking (same global chunk ids as the plain call)
+    e = launch_prefill(in, 0, o, s0a, bst, seg_cu, p.nseg, 0, p.total, HV, HQK, nch, ws, wsb,
+                       stream, 0, nullptr, 0);
+    if (e != hipSuccess) return e;
+    rec(1);
+    // pass 1a: B_j (and the first segments' final outputs)
+    e = launch_prefill(in, 0, o, s0a, bst, seg_cu, p.nseg, 0, p.total, HV, HQK, nch, ws, wsb,
+                       stream, 0, nullptr, 1);
+    if (e != hipSuccess) return e;
+    rec(2);
+    // pass 1b: Phi_j from v = 0 and S = I
+    const PrepIn in0 = plain_in(q, k, zv, g, beta);
+    e = launch_prefill(in0, 0, o_junk, s0i, phi, seg_cu, p.nseg, 0, p.total, HV, HQK, nch, ws,
+                       wsb, stream, 0, nullptr, 1);
+    if (e != hipSuccess) return e;
+    rec(3);
+    hipLaunchKernelGGL(twolevel_combine_kernel, dim3(p.nseq * HV * 8), dim3(256), 0, stream, phi,
+                       bst, seq_seg0, seq_seg0 + p.nseq, HV, E);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    rec(4);
+    // replay from the entry states, the first segments again from their
+    // initial state (s0a)
+    for (int s = 0; s < p.nseq; ++s) {
+        const size_t bytes = (size_t)HV * kSt * 4;
+        const size_t seg = (size_t)p.seq_seg0[s];
+        e = hipMemcpyAsync(E + seg * HV * kSt, s0a + seg * HV * kSt, bytes,
+                           hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess) return e;
+    }
+    e = launch_prefill(in, 0, o, E, sfr, seg_cu, p.nseg, 0, p.total, HV, HQK, nch, ws, wsb,
+                       stream, 0, nullptr, 1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(twolevel_gather_kernel, dim3(256), dim3(256), 0, stream, sfr,
+                       seq_seg0 + 2 * p.nseq, p.nseq, HV, final_state);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    rec(5);
+    return hipSuccess;
+}

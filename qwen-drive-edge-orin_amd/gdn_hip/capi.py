@@ -48,6 +48,9 @@ _PROTOS = {
                                     [vp, c_size_t, hipStream_t, ct.c_uint]),
     "deltanet_varlen_chunk_map": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
     "deltanet_varlen_chunks_before": (c_int, [vp, c_int, c_int, c_int, c_int]),
+    "deltanet_prefill_twolevel_workspace_size": (c_size_t, [vp, c_int, c_int, c_int, c_int]),
+    "deltanet_chunk_prefill_twolevel": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, vp] +
+                                        [c_int] * 5 + [vp, c_size_t, hipStream_t, vp, c_int]),
     "deltanet_varlen_locate_chunk": (c_int, [vp, c_int, c_int, c_int, c_int, vp]),
     "deltanet_chunk_prefill_varlen": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, i32p] +
                                       [c_int] * 7 + [vp, c_size_t, hipStream_t, c_int]),

@@ -243,3 +243,26 @@ def test_stream_probe_rejects_on_host(lib):
     assert lib.gdn_stream_probe(2, 1, p, None, p, 1024, 1, None) == INVALID
     assert lib.gdn_stream_probe(2, 1, p, p, p, 1024, 5, None) == INVALID
     assert lib.gdn_stream_probe(1, 0, None, None, None, 1024, 4, None) == INVALID
+
+
+def test_twolevel_rejects_on_host(lib):
+    """The two-level prototype's host checks: malformed host cu_seqlens (not
+    starting at 0, decreasing), a bad segment count, a short workspace and a
+    wrong event count are rejected before any launch."""
+    cu_ok = (ct.c_int32 * 3)(0, 100, 300)
+    p = ct.cast(cu_ok, ct.c_void_p)
+    size = lib.deltanet_prefill_twolevel_workspace_size(p, 2, 300, 4, 3)
+    assert size > 0
+    assert lib.deltanet_prefill_twolevel_workspace_size(None, 2, 150, 4, 3) > 0
+    for cu in ((5, 100, 300), (0, 200, 100)):
+        bad = (ct.c_int32 * 3)(*cu)
+        assert lib.deltanet_prefill_twolevel_workspace_size(ct.cast(bad, ct.c_void_p), 2, 300, 4,
+                                                            3) == 0
+    assert lib.deltanet_prefill_twolevel_workspace_size(p, 2, 300, 4, 0) == 0
+    d = 16
+    base = [d, d, d, d, d, d, None, d, p, 2, 300, 4, 2]
+    assert lib.deltanet_chunk_prefill_twolevel(*base, 3, d, size - 1, None, None, 0) == INVALID
+    assert lib.deltanet_chunk_prefill_twolevel(*base, 0, d, size, None, None, 0) == INVALID
+    assert lib.deltanet_chunk_prefill_twolevel(*base, 3, d, size, None, d, 5) == INVALID
+    assert lib.deltanet_chunk_prefill_twolevel(d, d, d, d, d, d, None, d, p, 2, 300, 4, 3, 3, d,
+                                               size, None, None, 0) == INVALID   # HV % HQK
