@@ -56,6 +56,22 @@ hipError_t deltanet_chunk_prefill_spin(const void* q, const void* k, const void*
                                        size_t workspace_bytes, hipStream_t stream,
                                        unsigned spin_limit);
 
+/* deltanet_chunk_prefill / _varlen (DK = DV = 128, chunk 64, dump_debug = 0)
+ * with the scan instance chosen by the caller: slice_cols 16 runs one scan
+ * work-group per 16 value columns of a (sequence, head), 32 the paired
+ * instance with one per 32 columns, 0 the library's own choice (16 while the
+ * 16-column groups fit on the device's CUs at once, 32 beyond).  Both give
+ * bitwise the same o and final state.  cu_seqlens NULL: num_seqs sequences of
+ * T tokens; otherwise a device array [num_seqs + 1] and T the total token
+ * count.  spin_limit 0 keeps the library's bounded-wait limit, otherwise as in
+ * deltanet_chunk_prefill_spin.  Other slice_cols: hipErrorInvalidValue. */
+hipError_t deltanet_chunk_prefill_cols(const void* q, const void* k, const void* v,
+                                       const float* g, const float* beta, void* o,
+                                       const float* initial_state, float* final_state,
+                                       const int32_t* cu_seqlens, int num_seqs, int T, int HV,
+                                       int HQK, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream, int slice_cols, unsigned spin_limit);
+
 /* Host mirror of the kernels' sequence bookkeeping for a packed batch
  * (host memory, no GPU involved): for each sequence s its first chunk id,
  * the chunks the scan processes (never past the workspace's chunk bound),

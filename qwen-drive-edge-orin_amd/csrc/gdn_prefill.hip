@@ -1707,6 +1707,37 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
     }
 }
 
+// The (sequence, v-head, k-head) of scan work-group pair index pidx (< N HV,
+// uniform over the group) and its sequence's token and chunk ranges.  Packed
+// sequences of different lengths: groups start in id order as CUs free up,
+// so the low pair indices go to the longest sequences (longest first).
+// seqsel and red are LDS scratch; every thread of the group calls this.
+__device__ inline void scan_context(const ScanArgs& a, int pidx, int* seqsel, int* red,
+                                    ScanCtx& x) {
+    const int tid = threadIdx.x;
+    x.seq = pidx / a.HV;
+    x.hv = pidx - x.seq * a.HV;
+    if (a.cu && a.N <= kScanThreads) {
+        if (tid < a.N) {
+            const int my = seq_count(a.cu, a.T, a.total, tid);
+            int rank = 0;
+            for (int u = 0; u < a.N; ++u) {
+                const int lu = seq_count(a.cu, a.T, a.total, u);
+                rank += (lu > my || (lu == my && u < tid)) ? 1 : 0;
+            }
+            if (rank == x.seq) *seqsel = tid;
+        }
+        __syncthreads();
+        x.seq = *seqsel;
+    }
+    x.hk = x.hv / (a.HV / a.HK);
+    x.len = seq_count(a.cu, a.T, a.total, x.seq);
+    x.tok_base = seq_lo(a.cu, a.T, a.total, x.seq);
+    x.chunk0 = __builtin_amdgcn_readfirstlane(
+        chunks_before<kScanThreads>(a.cu, a.T, a.total, x.seq, red));
+    x.nch = seq_chunks_bounded(a.cu, a.T, a.total, x.seq, x.chunk0, a.nch_bound);
+}
+
 // s0 and sf may be the same buffer: the chain reads its elements of the
 // initial state before its first chunk and writes the same elements after its
 // last, and no other wave touches either.
@@ -1730,29 +1761,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     x.sl = qd % kSlicesPerHead;
     const int pidx = (qd / kSlicesPerHead) * 8 + xcd;
     if (pidx >= a.N * a.HV) return;
-    x.seq = pidx / a.HV;
-    x.hv = pidx - x.seq * a.HV;
-    // Packed sequences of different lengths: groups start in id order as CUs
-    // free up, so the low ids go to the longest sequences (longest first).
-    if (a.cu && a.N <= kScanThreads) {
-        if (tid < a.N) {
-            const int my = seq_count(a.cu, a.T, a.total, tid);
-            int rank = 0;
-            for (int u = 0; u < a.N; ++u) {
-                const int lu = seq_count(a.cu, a.T, a.total, u);
-                rank += (lu > my || (lu == my && u < tid)) ? 1 : 0;
-            }
-            if (rank == x.seq) sm.seqsel = tid;
-        }
-        __syncthreads();
-        x.seq = sm.seqsel;
-    }
-    x.hk = x.hv / (a.HV / a.HK);
-    x.len = seq_count(a.cu, a.T, a.total, x.seq);
-    x.tok_base = seq_lo(a.cu, a.T, a.total, x.seq);
-    x.chunk0 = __builtin_amdgcn_readfirstlane(
-        chunks_before<kScanThreads>(a.cu, a.T, a.total, x.seq, sm.red));
-    x.nch = seq_chunks_bounded(a.cu, a.T, a.total, x.seq, x.chunk0, a.nch_bound);
+    scan_context(a, pidx, &sm.seqsel, sm.red, x);
     if (tid == 0) {
         lds_st(&sm.fill[0], 0);
         lds_st(&sm.fill[1], 0);
@@ -1802,6 +1811,572 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// paired scan kernel: one work-group (8 waves) per (32 value columns, v-head,
+// sequence), for calls whose 16-column work-groups outnumber the CUs (packed
+// or batched sequences).  The two 16-column halves of a group share its
+// ring-C stages (K^T, -W), the gates, the (T - I) fragments, Q and M, so a
+// chunk's operands cross from L2 to a CU once per 32 columns instead of once
+// per 16, and the call takes half the group-steps.  Each half's arithmetic is
+// the 16-column kernel's, operation for operation, so o and the final state
+// are bitwise the same.
+//
+//   chains    waves 0 and 1 (SIMDs 0 and 1): one 128 x 16 state slice each,
+//             the 16-column chain step.
+//   producer  wave 2: U of both halves.
+//   lo helper wave 3: Sc of both halves; K^T read once per chunk.
+//   loaders   waves 4 and 5 (beside the chains), chunks of even and odd
+//             index: K^T, -W, V of both halves and the gates record of chunk
+//             c into ring-C and ring-P stage c % 3 together.
+//   outputs   waves 6 and 7, chunks of even and odd index: O of both halves.
+//
+// LDS, 163,168 of 163,840 bytes: ring C 3 x 32 KB, ring P 3 x 5 KB, a U ring
+// 2 x 8 KB, 2 hand-off slots x 12 KB and one lo slot of 8 KB.  The helper's
+// final Sc (16 KB) goes to ring-C stage nch % 3, which no chunk uses by then.
+// ---------------------------------------------------------------------------
+constexpr int kPairCols = 2 * kSliceCols;            // 32
+constexpr int kPairsPerHead = kDV / kPairCols;       // 4
+constexpr int kRingP2 = kRingC;   // V of both halves and gates, with ring C's stage
+constexpr int kRingU2 = 2;        // U of both halves
+constexpr int kHand2 = 2;         // chain -> output hand-off slots
+static_assert(kHand2 % 2 == 0, "a hand-off slot is reused by a chunk of the same parity");
+
+struct StageP2 {
+    u32x4 V[2][kChunk * 2];   // per half: V rows of its 16 columns, 2 pieces per row
+    float gates[256];         // gates record
+};
+
+struct StageU2 {
+    f32x4 U[2][4][64];        // per half: U, D layout per row tile
+};
+
+struct Hand2 {
+    half8 S[2][4][64];        // per half: S at the chunk's start, fp16 B fragments
+    half8 V[2][2][64];        // per half: V_n, fp16 B fragments
+};
+
+struct LoHand2 {
+    f32x4 d[2][4][64];        // per half: d o V_n (fp32, D layout per row tile)
+    float gam;                // e^{c63} of the chunk
+    float pad_[63];
+};
+
+struct ScanSmem2 {
+    StageC c[kRingC];
+    StageP2 p[kRingP2];
+    StageU2 u[kRingU2];
+    Hand2 h[kHand2];
+    LoHand2 lo;
+    int fill[2];      // per loader: chunks of its parity whose ring-C and ring-P loads have landed
+    int uready;       // chunks whose U (both halves) is in the U ring
+    int freeC[2];     // per chain: chunks whose ring-C, ring-P and U stages it has finished reading
+    int kfree;        // chunks whose ring-C K^T the lo helper has finished reading
+    int ready[2];     // per chain: chunks whose hand-off half it has written
+    int cons[2];      // per output wave: chunks of its parity whose hand-off slot it has read
+    int dvready[2];   // per chain: chunks whose d o V_n half is in the lo slot
+    int lodone;       // chunks whose lo slot the helper has read
+    int scdone;       // the helper's Sc is in ring-C stage nch % 3
+    int abort;        // a bounded wait ran out: every wave stops
+    int seqsel;
+    int red[kScanWaves];
+};
+static_assert(sizeof(ScanSmem2) <= 160 * 1024, "paired scan LDS");
+static_assert(sizeof(StageC) >= 2 * 8 * 64 * sizeof(f32x4), "a ring-C stage holds both halves' Sc");
+
+// Loader j (0 or 1) takes the chunks c of parity j: once stage c % 3 is free
+// (chunk c - 3 read by both chains, the lo helper and the producer), one group
+// of direct-to-LDS loads for chunk c: K^T (16), -W (16), V of both halves (4)
+// and the gates record (1), published when all have landed.
+__device__ void run_loader2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                            int j, int lane) {
+    if (x.nch <= 0) return;
+    for (int c = j; c < x.nch; c += 2) {
+        const int need = c - kRingC + 1;
+        if (!w.until([&] {
+                const bool f0 = lds_ld(&sm.freeC[0]) >= need;
+                const bool f1 = lds_ld(&sm.freeC[1]) >= need;
+                const bool fk = lds_ld(&sm.kfree) >= need;
+                const bool fu = lds_ld(&sm.uready) >= need;
+                return f0 & f1 & fk & fu;
+            }))
+            break;
+        asm volatile("" ::: "memory");
+        const size_t ch = (size_t)(x.chunk0 + c) * a.HV + x.hv;
+        StageC& st = sm.c[c % kRingC];
+        const u32x4* ksrc = a.ws.KT + ((size_t)(x.chunk0 + c) * a.HK + x.hk) * (16 * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < 16; ++f) lds_dma16(ksrc + f * 64, &st.KT[f][0]);
+        const half8* wsrc = a.ws.W + ch * (16 * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < 16; ++f) lds_dma16(wsrc + f * 64, &st.W[f][0]);
+        StageP2& sp = sm.p[c % kRingP2];
+        const int t0 = x.tok_base + c * kChunk, rows = min(kChunk, x.len - c * kChunk);
+        // V: slot 64 i + lane of half h -> row (64 i + lane) / 2, piece lane % 2
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int s = 64 * i + lane, r = min(s >> 1, rows - 1);
+                lds_dma16(a.in.v + ((size_t)(t0 + r) * a.HV + x.hv) * kDV + kPairCols * x.sl +
+                              kSliceCols * h + 8 * (s & 1),
+                          &sp.V[h][64 * i]);
+            }
+        }
+        lds_dma16(a.ws.gates + ch * (kGateBytes / 4) + 4 * lane, &sp.gates[0]);
+        vm_wait_all();
+        if (lane == 0) lds_st(&sm.fill[j], (c >> 1) + 1);
+    }
+    vm_wait_all();   // no load may land in LDS after the group ends
+}
+
+// Producer: U = beta V + (T - I)(beta V) for both halves, the 16-column
+// producer's products per half; (T - I) fragments two chunks ahead in two
+// register sets used in turn.  U stage c % 2 is written once both chains have
+// finished chunk c - 2.
+template <int kRaw>
+__device__ void run_producer2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w,
+                              const ScanCtx& x, int lane) {
+    const int lg = lane >> 4, lm = lane & 15;
+    auto load_t = [&](int c, half8 (&h)[kTri], half8 (&l)[kTri]) {
+        const int cc = min(c, x.nch - 1);
+        const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
+        const half8* ph = a.ws.TI + ch * (kTri * 64) + lane;
+        const half8* pl = a.ws.TIlo + ch * (kTri * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < kTri; ++f) {
+            h[f] = ph[f * 64];
+            l[f] = pl[f * 64];
+        }
+    };
+    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri]) -> bool {
+        if (!w.until([&] {
+                const bool f = lds_ld(&sm.fill[c & 1]) >= (c >> 1) + 1;
+                const bool u0 = lds_ld(&sm.freeC[0]) >= c - kRingU2 + 1;
+                const bool u1 = lds_ld(&sm.freeC[1]) >= c - kRingU2 + 1;
+                return f & u0 & u1;
+            }))
+            return false;
+        asm volatile("" ::: "memory");
+        const StageP2& st = sm.p[c % kRingP2];
+        StageU2& su = sm.u[c % kRingU2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // X = beta V, as the 16-column producer forms it
+            f32x4 X[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const f32x4 be = *reinterpret_cast<const f32x4*>(&st.gates[kGBeta + 16 * mt + 4 * lg]);
+                const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(st.V[h]) +
+                                       (16 * mt + 4 * lg + (lm >> 2)) * kSliceCols + 4 * (lm & 3);
+                const s16x4 vt = lds_read_tr(vsrc);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) X[mt][i] = be[i] * v16_to_f32<kRaw>((uint16_t)vt[i]);
+            }
+            half8 xh[2], xl[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) split_hilo8(X[2 * kb], X[2 * kb + 1], xh[kb], xl[kb]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                f32x4 U = X[mt];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    if (kb > mt / 2) break;
+                    const int f = tri_base(mt) + kb;
+                    U = mfma16(th[f], xh[kb], U);
+                    U = mfma16(th[f], xl[kb], U);
+                    U = mfma16(tl[f], xh[kb], U);
+                }
+                su.U[h][mt][lane] = U;
+            }
+        }
+        // the products have read this set: chunk c + 2's fragments go in
+        load_t(c + 2, th, tl);
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.uready, c + 1);
+        return true;
+    };
+    if (x.nch <= 0) return;
+    half8 t0h[kTri], t0l[kTri], t1h[kTri], t1l[kTri];
+    load_t(0, t0h, t0l);
+    load_t(1, t1h, t1l);
+    // step() is false only when a bounded wait gave up
+    for (int c = 0; c < x.nch; c += 2) {
+        if (!step(c, t0h, t0l)) return;
+        if (c + 1 < x.nch && !step(c + 1, t1h, t1l)) return;
+    }
+}
+
+// Chain of half hh: the 16-column chain step on columns 32 sl + 16 hh ..
+// + 15, with the paired kernel's stages and per-half counters.
+__device__ void run_chain2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                           int hh, int lane) {
+    const int lg = lane >> 4, lm = lane & 15;
+    const int col = kPairCols * x.sl + kSliceCols * hh + lm;
+    auto dk_of = [&](int t, int i) { return 32 * (t >> 1) + 8 * lg + 4 * (t & 1) + i; };
+    const size_t sbase = ((size_t)x.seq * a.HV + x.hv) * kDK * kDV + col;
+
+    f32x4 S[8];
+    if (a.s0) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[t][i] = a.s0[sbase + (size_t)dk_of(t, i) * kDV];
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) S[t] = zero4();
+    }
+    half8 S16[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) S16[kb] = cat8(to_half4(S[2 * kb]), to_half4(S[2 * kb + 1]));
+
+    bool ok = true;
+    for (int c = 0; c < x.nch; ++c) {
+        const int hs = c % kHand2;
+        StageC& sc = sm.c[c % kRingC];
+        StageP2& sp = sm.p[c % kRingP2];
+        StageU2& su = sm.u[c % kRingU2];
+        auto ready = [&] {   // every counter loaded, no short-circuit: one round trip
+            const bool f = lds_ld(&sm.fill[c & 1]) >= (c >> 1) + 1;
+            const bool u = lds_ld(&sm.uready) >= c + 1;
+            const bool h = lds_ld(&sm.cons[c & 1]) >= (c >= kHand2 ? ((c - kHand2) >> 1) + 1 : 0);
+            const bool l = lds_ld(&sm.lodone) >= c;   // the one lo slot held chunk c - 1
+            return f & u & h & l;
+        };
+        // (1) U, -W and the gates, read together with the counters (as in the
+        // 16-column chain)
+        f32x4 Vn[4], dec[4];
+        half8 wf[16];
+        float c63;
+        auto read_operands = [&] {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) Vn[mt] = su.U[hh][mt][lane];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) wf[mt * 4 + kb] = sc.W[mt * 4 + kb][lane];
+            }
+            c63 = sp.gates[kGC63];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                dec[mt] = *reinterpret_cast<const f32x4*>(&sp.gates[kGDec + 16 * mt + 4 * lg]);
+        };
+        const bool early = ready();
+        asm volatile("" ::: "memory");
+        read_operands();
+        if (!early) {
+            ok = w.until(ready);
+            if (!ok) break;
+            asm volatile("" ::: "memory");
+            read_operands();
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // (2) V_n = U + (-W) S16
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) Vn[mt] = mfma16(wf[mt * 4 + kb], S16[kb], Vn[mt]);
+        }
+        // (3) K^T operands of the state update
+        bf16x8 kt[8][2];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) kt[t][kb] = __builtin_bit_cast(bf16x8, sc.KT[t * 2 + kb][lane]);
+        }
+        // (4) decay; S at the chunk's start to the hand-off slot
+        const float gam = __builtin_amdgcn_exp2f(c63 * kLog2e);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) sm.h[hs].S[hh][kb][lane] = S16[kb];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) S[t] = S[t] * gam;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS read
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // (5) d o V_n, hi part (bf16)
+        f32x4 dv[4];
+        u32x4 hw[2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            dv[mt] = dec[mt] * Vn[mt];
+            asm volatile("" : "+v"(dv[mt]));
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int p = 0; p < 2; ++p)
+                    hw[kb][2 * h + p] = pack_bf16x2(dv[2 * kb + h][2 * p], dv[2 * kb + h][2 * p + 1]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (6) d o V_n and the decay to the lo helper
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) sm.lo.d[hh][mt][lane] = dv[mt];
+        if (hh == 0 && lane == 0) sm.lo.gam = gam;
+        // (7) S' = e^{c63} S + K^T hi
+        half8 vh[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf16x8 hi = __builtin_bit_cast(bf16x8, hw[kb]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                S[t] = mfma16_bf16(kt[t][kb], hi, S[t]);
+                if (kb == 0 && t < 2) vh[t] = cat8(to_half4(Vn[2 * t]), to_half4(Vn[2 * t + 1]));
+                if (kb == 1 && (t & 1))
+                    S16[t >> 1] = cat8(to_half4(S[t - 1]), to_half4(S[t]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // (8) hand-off of V_n (fp16) for the output
+        sm.h[hs].V[hh][0][lane] = vh[0];
+        sm.h[hs].V[hh][1][lane] = vh[1];
+        __builtin_amdgcn_sched_barrier(0);
+        lds_wait_all();
+        if (lane == 0) {
+            lds_st(&sm.ready[hh], c + 1);
+            lds_st(&sm.freeC[hh], c + 1);
+            lds_st(&sm.dvready[hh], c + 1);
+        }
+    }
+    if (!ok) return;
+    f32x4 Sc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) Sc[t] = zero4();
+    if (x.nch > 0) {
+        // the helper's Sc, left in ring-C stage nch % 3 after its last chunk
+        if (!w.until([&] { return lds_ld(&sm.scdone) != 0; })) return;
+        asm volatile("" ::: "memory");
+        const f32x4* src = reinterpret_cast<const f32x4*>(&sm.c[x.nch % kRingC]) + hh * 8 * 64;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) Sc[t] = src[t * 64 + lane];
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a.sf[sbase + (size_t)dk_of(t, i) * kDV] = S[t][i] + Sc[t][i];
+    }
+}
+
+// Lo helper: the 16-column helper's work for both halves, K^T read once per
+// chunk from its ring-C stage.
+__device__ void run_lo_helper2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w,
+                               const ScanCtx& x, int lane) {
+    if (x.nch <= 0) return;
+    f32x4 Sc[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) Sc[h][t] = zero4();
+    }
+    for (int c = 0; c < x.nch; ++c) {
+        if (!w.until([&] {
+                const bool d0 = lds_ld(&sm.dvready[0]) >= c + 1;
+                const bool d1 = lds_ld(&sm.dvready[1]) >= c + 1;
+                return d0 & d1;
+            }))
+            return;
+        asm volatile("" ::: "memory");
+        const StageC& sc = sm.c[c % kRingC];
+        f32x4 d[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) d[h][mt] = sm.lo.d[h][mt][lane];
+        }
+        const float gam = sm.lo.gam;
+        u32x4 kc[16];
+#pragma unroll
+        for (int f = 0; f < 16; ++f) kc[f] = sc.KT[f][lane];
+        lds_wait_all();
+        if (lane == 0) {
+            lds_st(&sm.lodone, c + 1);
+            lds_st(&sm.kfree, c + 1);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            bf16x8 lo[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                u32x4 lw;
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        const f32x4& dd = d[h][2 * kb + g];
+                        const uint32_t hp = pack_bf16x2(dd[2 * p], dd[2 * p + 1]);
+                        const float r0 = dd[2 * p] - __uint_as_float(hp << 16);
+                        const float r1 = dd[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
+                        lw[2 * g + p] = pack_bf16x2(r0, r1);
+                    }
+                }
+                lo[kb] = __builtin_bit_cast(bf16x8, lw);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) Sc[h][t] = Sc[h][t] * gam;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    Sc[h][t] = mfma16_bf16(__builtin_bit_cast(bf16x8, kc[t * 2 + kb]), lo[kb], Sc[h][t]);
+            }
+        }
+    }
+    // every chunk is done: no wave reads ring-C stage nch % 3 (it last held
+    // chunk nch - 3, which both chains and this wave have finished) and no
+    // loader fills it again
+    f32x4* dst = reinterpret_cast<f32x4*>(&sm.c[x.nch % kRingC]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dst[(h * 8 + t) * 64 + lane] = Sc[h][t];
+    }
+    lds_wait_all();
+    if (lane == 0) lds_st(&sm.scdone, 1);
+}
+
+// Output wave j: O of both halves for the chunks of parity j, the 16-column
+// output's products per half; Q, M and s e^c are shared by the halves.
+template <int kRaw>
+__device__ void run_output2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
+                            int j, int lane) {
+    const int lg = lane >> 4, lm = lane & 15;
+    half8 qf[16], mf[kTri];
+    float es[4];
+    auto load = [&](int c) {
+        const int cc = min(c, x.nch - 1);
+        const size_t ch = (size_t)(x.chunk0 + cc) * a.HV + x.hv;
+        const half8* qq = a.ws.Q + ((size_t)(x.chunk0 + cc) * a.HK + x.hk) * (16 * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < 16; ++f) qf[f] = qq[f * 64];
+        const half8* mm = a.ws.M + ch * (kTri * 64) + lane;
+#pragma unroll
+        for (int f = 0; f < kTri; ++f) mf[f] = mm[f * 64];
+        const float* gr = a.ws.gates + ch * (kGateBytes / 4) + kGSec + lm;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) es[mt] = gr[16 * mt];
+    };
+    if (j >= x.nch) return;
+    load(j);
+    for (int c = j; c < x.nch; c += 2) {
+        const int hs = c % kHand2;
+        if (!w.until([&] {
+                const bool r0 = lds_ld(&sm.ready[0]) >= c + 1;
+                const bool r1 = lds_ld(&sm.ready[1]) >= c + 1;
+                return r0 & r1;
+            }))
+            return;
+        asm volatile("" ::: "memory");
+        half8 hsf[2][4], hvf[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) hsf[h][kb] = sm.h[hs].S[h][kb][lane];
+            hvf[h][0] = sm.h[hs].V[h][0][lane];
+            hvf[h][1] = sm.h[hs].V[h][1][lane];
+        }
+        lds_wait_all();
+        if (lane == 0) lds_st(&sm.cons[j], (c >> 1) + 1);
+        f32x4 ov[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) ov[h][mt] = zero4();
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) ov[h][mt] = mfma16(hsf[h][kb], qf[mt * 4 + kb], ov[h][mt]);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                ov[h][mt] = ov[h][mt] * es[mt];
+                ov[h][mt] = mfma16(hvf[h][0], mf[tri_base(mt)], ov[h][mt]);
+                if (mt >= 2) ov[h][mt] = mfma16(hvf[h][1], mf[tri_base(mt) + 1], ov[h][mt]);
+            }
+        }
+        // the products have read Q, M and s e^c: the next chunk's go out now
+        asm volatile("" : "+v"(ov[0][0]), "+v"(ov[0][1]), "+v"(ov[0][2]), "+v"(ov[0][3]),
+                     "+v"(ov[1][0]), "+v"(ov[1][1]), "+v"(ov[1][2]), "+v"(ov[1][3]));
+        load(c + 2);
+        const int rows = min(kChunk, x.len - c * kChunk);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int r = 16 * mt + lm;
+                uint32_t b[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    b[e] = f32_to_bf16_bits(ov[h][mt][e]);
+                    if constexpr (kRaw == 2) b[e] = f16_bits(__uint_as_float(b[e] << 16));
+                }
+                if (r < rows) {
+                    uint2* dst = reinterpret_cast<uint2*>(
+                        a.o + ((size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv) * kDV +
+                        kPairCols * x.sl + kSliceCols * h + 4 * lg);
+                    *dst = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+                }
+            }
+        }
+    }
+}
+
+template <int kRaw>
+__global__ __launch_bounds__(kScanThreads, 1) void gdn_scan2_kernel(ScanArgs a) {
+    __shared__ ScanSmem2 sm;
+    // kernel-argument lines requested together (as in gdn_scan_kernel)
+    asm volatile("" ::"s"(a.in.q), "s"(a.in.beta), "s"(a.in.dt_bias), "s"(a.ws.M), "s"(a.ws.KT),
+                 "s"(a.ws.dbgT), "s"(a.ws.dbgC), "s"(a.z), "s"(a.s0), "s"(a.N), "s"(a.HK),
+                 "s"(a.spin));
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    // XCD-aware id: the four groups of one (sequence, head) share id % 8
+    const int id = blockIdx.x;
+    const int xcd = id & 7, qd = id >> 3;
+    ScanCtx x;
+    x.sl = qd % kPairsPerHead;
+    const int pidx = (qd / kPairsPerHead) * 8 + xcd;
+    if (pidx >= a.N * a.HV) return;
+    scan_context(a, pidx, &sm.seqsel, sm.red, x);
+    if (tid == 0) {
+        lds_st(&sm.fill[0], 0);
+        lds_st(&sm.fill[1], 0);
+        lds_st(&sm.uready, 0);
+        lds_st(&sm.freeC[0], 0);
+        lds_st(&sm.freeC[1], 0);
+        lds_st(&sm.kfree, 0);
+        lds_st(&sm.ready[0], 0);
+        lds_st(&sm.ready[1], 0);
+        lds_st(&sm.cons[0], 0);
+        lds_st(&sm.cons[1], 0);
+        lds_st(&sm.dvready[0], 0);
+        lds_st(&sm.dvready[1], 0);
+        lds_st(&sm.lodone, 0);
+        lds_st(&sm.scdone, 0);
+        lds_st(&sm.abort, 0);
+    }
+    __syncthreads();
+    const Waiter w{&sm.abort, a.ws.status, a.spin};
+    // wave w runs on SIMD w % 4: each chain shares its SIMD with a loader
+    switch (wave) {
+        case 0: run_chain2(sm, a, w, x, 0, lane); break;
+        case 1: run_chain2(sm, a, w, x, 1, lane); break;
+        case 2: run_producer2<kRaw>(sm, a, w, x, lane); break;
+        case 3: run_lo_helper2(sm, a, w, x, lane); break;
+        case 4: run_loader2(sm, a, w, x, 0, lane); break;
+        case 5: run_loader2(sm, a, w, x, 1, lane); break;
+        case 6: run_output2<kRaw>(sm, a, w, x, 0, lane); break;
+        default: run_output2<kRaw>(sm, a, w, x, 1, lane); break;
+    }
+}
+
 // raw: 0 for prepared inputs, 1 / 2 for raw bf16 / fp16 q, k (normalised in
 // the prep; then v and o have that dtype too).
 // The gated-RMSNorm epilogue's inputs (bf16 z [token][HV][128], bf16 weight
@@ -1817,6 +2392,38 @@ inline long long scan_groups(int N, int HV) {
     return (long long)((N * HV + 7) / 8) * 8 * kSlicesPerHead;
 }
 
+// ... and of the paired instance (32 columns per group).
+inline long long scan2_groups(int N, int HV) {
+    return (long long)((N * HV + 7) / 8) * 8 * kPairsPerHead;
+}
+
+// CUs of the current device (cached per device; 256 if the query fails).
+int device_cus() {
+    constexpr int kDevs = 64;
+    static int cached[kDevs] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 256;
+    int n = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
+    }
+    return n;
+}
+
+// Scan instance: 16-column groups while they fit on the CUs at once (one
+// group per CU), the paired 32-column groups once they would run in rounds
+// (then the halves' shared operands halve the rounds).  cols forces 16 or 32
+// (diagnostics); the debug dump and the norm epilogue exist in the 16-column
+// instance only.
+bool use_pair_scan(int cols, int N, int HV, int dump_debug, bool norm) {
+    if (cols == 32) return true;
+    if (cols == 16 || dump_debug || norm) return false;
+    return (long long)N * HV * kSlicesPerHead > device_cus();
+}
+
 // The norm epilogue's work-groups wait on each other, so its scan is launched
 // cooperatively (all groups resident at once, or no launch at all); norm !=
 // nullptr requires it.
@@ -1825,7 +2432,9 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
                           hipStream_t stream, int dump_debug, hipEvent_t* ev = nullptr,
                           int only = -1, unsigned spin = kDefaultSpin,
-                          const NormIn* norm = nullptr) {
+                          const NormIn* norm = nullptr, int cols = 0) {
+    const bool pair = use_pair_scan(cols, N, HV, dump_debug, norm != nullptr);
+    if (pair && (dump_debug || norm)) return hipErrorInvalidValue;
     const WsLayout L(nch_bound * (size_t)HV);
     const size_t need = dump_debug ? L.total : L.live;
     if (workspace_bytes < need) return hipErrorInvalidValue;
@@ -1885,9 +2494,13 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
         sa.nw = norm->w;
         sa.eps = norm->eps;
     }
-    const unsigned grid = (unsigned)scan_groups(N, HV);
+    const unsigned grid = (unsigned)(pair ? scan2_groups(N, HV) : scan_groups(N, HV));
     hipError_t err;
-    if (norm) {
+    if (pair) {
+        auto scan = raw == 1 ? gdn_scan2_kernel<1> : raw == 2 ? gdn_scan2_kernel<2> : gdn_scan2_kernel<0>;
+        hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), 0, stream, sa);
+        err = hipGetLastError();
+    } else if (norm) {
         void* kargs[] = {&sa};
         err = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(gdn_scan_kernel<0, false, true>),
                                          dim3(grid), dim3(kScanThreads), kargs, 0, stream);
@@ -2061,6 +2674,32 @@ extern "C" hipError_t deltanet_chunk_prefill_spin(const void* q, const void* k, 
     return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr, B,
                           T, B * T, HV, HQK, nc, workspace, workspace_bytes, stream, 0, nullptr,
                           -1, spin_limit);
+}
+
+extern "C" hipError_t deltanet_chunk_prefill_cols(const void* q, const void* k, const void* v,
+                                                  const float* g, const float* beta, void* o,
+                                                  const float* initial_state, float* final_state,
+                                                  const int32_t* cu_seqlens, int num_seqs, int T,
+                                                  int HV, int HQK, void* workspace,
+                                                  size_t workspace_bytes, hipStream_t stream,
+                                                  int slice_cols, unsigned spin_limit) {
+    if (slice_cols != 0 && slice_cols != kSliceCols && slice_cols != kPairCols)
+        return hipErrorInvalidValue;
+    if (!dims_ok(HV, HQK, kDK, kDV, kChunk) || num_seqs <= 0 || T < 0) return hipErrorInvalidValue;
+    if (workspace == nullptr || final_state == nullptr) return hipErrorInvalidValue;
+    if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return hipErrorInvalidValue;
+    const unsigned spin = spin_limit ? spin_limit : kDefaultSpin;
+    if (cu_seqlens) {
+        const size_t nc = ((size_t)T + (size_t)(kChunk - 1) * num_seqs) / kChunk;
+        return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state,
+                              cu_seqlens, num_seqs, 0, T, HV, HQK, nc, workspace, workspace_bytes,
+                              stream, 0, nullptr, -1, spin, nullptr, slice_cols);
+    }
+    if ((long long)num_seqs * T > 0x7fffffffLL) return hipErrorInvalidValue;
+    const size_t nc = (size_t)num_seqs * ((T + kChunk - 1) / kChunk);
+    return launch_prefill(plain_in(q, k, v, g, beta), 0, o, initial_state, final_state, nullptr,
+                          num_seqs, T, num_seqs * T, HV, HQK, nc, workspace, workspace_bytes,
+                          stream, 0, nullptr, -1, spin, nullptr, slice_cols);
 }
 
 extern "C" int deltanet_prefill_kernel_count(void) { return kPrefillKernels; }

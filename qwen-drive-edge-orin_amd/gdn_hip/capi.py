@@ -46,6 +46,8 @@ _PROTOS = {
     "deltanet_prefill_status": (hipError_t, [vp, c_size_t, hipStream_t]),
     "deltanet_chunk_prefill_spin": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp] + [c_int] * 4 +
                                     [vp, c_size_t, hipStream_t, ct.c_uint]),
+    "deltanet_chunk_prefill_cols": (hipError_t, [vp, vp, vp, fp, fp, vp, fp, fp, vp] + [c_int] * 4 +
+                                    [vp, c_size_t, hipStream_t, c_int, ct.c_uint]),
     "deltanet_varlen_chunk_map": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
     "deltanet_varlen_chunks_before": (c_int, [vp, c_int, c_int, c_int, c_int]),
     "deltanet_prefill_twolevel_workspace_size": (c_size_t, [vp, c_int, c_int, c_int, c_int]),

@@ -266,3 +266,24 @@ def test_twolevel_rejects_on_host(lib):
     assert lib.deltanet_chunk_prefill_twolevel(*base, 3, d, size, None, d, 5) == INVALID
     assert lib.deltanet_chunk_prefill_twolevel(d, d, d, d, d, d, None, d, p, 2, 300, 4, 3, 3, d,
                                                size, None, None, 0) == INVALID   # HV % HQK
+
+
+def test_cols_entry_rejects_on_host(lib):
+    """deltanet_chunk_prefill_cols: a slice width other than 0, 16 or 32, bad
+    head counts, no sequences, a short workspace and missing pointers are
+    rejected before any launch."""
+    d = 16
+    wsb = lib.deltanet_prefill_live_workspace_size(2, 64, 4, 128, 128, 64)
+    base = [d, d, d, d, d, d, None, d, None, 2, 64, 4, 2, d, wsb, None]
+    for cols in (8, 24, 48, 64, -16, 1):
+        assert lib.deltanet_chunk_prefill_cols(*base, cols, 0) == INVALID
+    assert lib.deltanet_chunk_prefill_cols(d, d, d, d, d, d, None, d, None, 2, 64, 4, 3, d, wsb,
+                                           None, 32, 0) == INVALID          # HV % HQK
+    assert lib.deltanet_chunk_prefill_cols(d, d, d, d, d, d, None, d, None, 0, 64, 4, 2, d, wsb,
+                                           None, 32, 0) == INVALID          # no sequences
+    assert lib.deltanet_chunk_prefill_cols(d, d, d, d, d, d, None, d, None, 2, 64, 4, 2, d, wsb - 1,
+                                           None, 32, 0) == INVALID          # short workspace
+    assert lib.deltanet_chunk_prefill_cols(d, d, None, d, d, d, None, d, None, 2, 64, 4, 2, d, wsb,
+                                           None, 16, 0) == INVALID          # no v
+    assert lib.deltanet_chunk_prefill_cols(d, d, d, d, d, d, None, None, None, 2, 64, 4, 2, d, wsb,
+                                           None, 0, 0) == INVALID           # no final state
