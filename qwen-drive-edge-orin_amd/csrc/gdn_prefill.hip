@@ -1822,7 +1822,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
 // are bitwise the same.
 //
 //   chains    waves 0 and 1 (SIMDs 0 and 1): one 128 x 16 state slice each,
-//             the 16-column chain step.
+//             the 16-column chain step; each also forms its half's bf16 lo
+//             residual of d o V_n for the helper (the 16-column helper's own
+//             arithmetic, moved so that two chunks fit the lo slots).
 //   producer  wave 2: U of both halves.
 //   lo helper wave 3: Sc of both halves; K^T read once per chunk.
 //   loaders   waves 4 and 5 (beside the chains), chunks of even and odd
@@ -1830,8 +1832,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
 //             c into ring-C and ring-P stage c % 3 together.
 //   outputs   waves 6 and 7, chunks of even and odd index: O of both halves.
 //
-// LDS, 163,168 of 163,840 bytes: ring C 3 x 32 KB, ring P 3 x 5 KB, a U ring
-// 2 x 8 KB, 2 hand-off slots x 12 KB and one lo slot of 8 KB.  The helper's
+// LDS, 162,920 of 163,840 bytes: ring C 3 x 32 KB, ring P 3 x 5 KB, a U ring
+// 2 x 8 KB, 2 hand-off slots x 12 KB and 2 lo slots x 4 KB.  The helper's
 // final Sc (16 KB) goes to ring-C stage nch % 3, which no chunk uses by then.
 // ---------------------------------------------------------------------------
 constexpr int kPairCols = 2 * kSliceCols;            // 32
@@ -1856,24 +1858,24 @@ struct Hand2 {
 };
 
 struct LoHand2 {
-    f32x4 d[2][4][64];        // per half: d o V_n (fp32, D layout per row tile)
-    float gam;                // e^{c63} of the chunk
-    float pad_[63];
+    u32x4 lw[2][2][64];       // per half, k-block: bf16 lo residual of d o V_n (B operand)
 };
+constexpr int kLoSlots2 = 2;  // chain -> lo-helper hand-off slots
 
 struct ScanSmem2 {
     StageC c[kRingC];
     StageP2 p[kRingP2];
     StageU2 u[kRingU2];
     Hand2 h[kHand2];
-    LoHand2 lo;
+    LoHand2 lo[kLoSlots2];
+    float gam[kLoSlots2];    // e^{c63} of the chunk in each lo slot
     int fill[2];      // per loader: chunks of its parity whose ring-C and ring-P loads have landed
     int uready;       // chunks whose U (both halves) is in the U ring
     int freeC[2];     // per chain: chunks whose ring-C, ring-P and U stages it has finished reading
     int kfree;        // chunks whose ring-C K^T the lo helper has finished reading
     int ready[2];     // per chain: chunks whose hand-off half it has written
     int cons[2];      // per output wave: chunks of its parity whose hand-off slot it has read
-    int dvready[2];   // per chain: chunks whose d o V_n half is in the lo slot
+    int dvready[2];   // per chain: chunks whose lo residual half is in its lo slot
     int lodone;       // chunks whose lo slot the helper has read
     int scdone;       // the helper's Sc is in ring-C stage nch % 3
     int abort;        // a bounded wait ran out: every wave stops
@@ -2040,7 +2042,7 @@ __device__ void run_chain2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, co
             const bool f = lds_ld(&sm.fill[c & 1]) >= (c >> 1) + 1;
             const bool u = lds_ld(&sm.uready) >= c + 1;
             const bool h = lds_ld(&sm.cons[c & 1]) >= (c >= kHand2 ? ((c - kHand2) >> 1) + 1 : 0);
-            const bool l = lds_ld(&sm.lodone) >= c;   // the one lo slot held chunk c - 1
+            const bool l = lds_ld(&sm.lodone) >= c - kLoSlots2 + 1;
             return f & u & h & l;
         };
         // (1) U, -W and the gates, read together with the counters (as in the
@@ -2117,10 +2119,25 @@ __device__ void run_chain2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, co
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        // (6) d o V_n and the decay to the lo helper
+        // (6) the bf16 lo residual of d o V_n and the decay to the lo helper
+        {
+            LoHand2& lh = sm.lo[c % kLoSlots2];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) sm.lo.d[hh][mt][lane] = dv[mt];
-        if (hh == 0 && lane == 0) sm.lo.gam = gam;
+            for (int kb = 0; kb < 2; ++kb) {
+                u32x4 lw;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int h = q >> 1, p = q & 1;
+                    const f32x4& d = dv[2 * kb + h];
+                    const uint32_t hp = hw[kb][q];
+                    const float r0 = d[2 * p] - __uint_as_float(hp << 16);
+                    const float r1 = d[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
+                    lw[q] = pack_bf16x2(r0, r1);
+                }
+                lh.lw[hh][kb][lane] = lw;
+            }
+            if (hh == 0 && lane == 0) sm.gam[c % kLoSlots2] = gam;
+        }
         // (7) S' = e^{c63} S + K^T hi
         half8 vh[2];
 #pragma unroll
@@ -2165,8 +2182,8 @@ __device__ void run_chain2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, co
     }
 }
 
-// Lo helper: the 16-column helper's work for both halves, K^T read once per
-// chunk from its ring-C stage.
+// Lo helper: Sc <- e^{c63} Sc + K^T lo for both halves, with the lo residuals
+// the chains formed and K^T read once per chunk from its ring-C stage.
 __device__ void run_lo_helper2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w,
                                const ScanCtx& x, int lane) {
     if (x.nch <= 0) return;
@@ -2185,13 +2202,14 @@ __device__ void run_lo_helper2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w
             return;
         asm volatile("" ::: "memory");
         const StageC& sc = sm.c[c % kRingC];
-        f32x4 d[2][4];
+        const LoHand2& lh = sm.lo[c % kLoSlots2];
+        u32x4 lwv[2][2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) d[h][mt] = sm.lo.d[h][mt][lane];
+            for (int kb = 0; kb < 2; ++kb) lwv[h][kb] = lh.lw[h][kb][lane];
         }
-        const float gam = sm.lo.gam;
+        const float gam = sm.gam[c % kLoSlots2];
         u32x4 kc[16];
 #pragma unroll
         for (int f = 0; f < 16; ++f) kc[f] = sc.KT[f][lane];
@@ -2204,21 +2222,7 @@ __device__ void run_lo_helper2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w
         for (int h = 0; h < 2; ++h) {
             bf16x8 lo[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                u32x4 lw;
-#pragma unroll
-                for (int g = 0; g < 2; ++g) {
-#pragma unroll
-                    for (int p = 0; p < 2; ++p) {
-                        const f32x4& dd = d[h][2 * kb + g];
-                        const uint32_t hp = pack_bf16x2(dd[2 * p], dd[2 * p + 1]);
-                        const float r0 = dd[2 * p] - __uint_as_float(hp << 16);
-                        const float r1 = dd[2 * p + 1] - __uint_as_float(hp & 0xffff0000u);
-                        lw[2 * g + p] = pack_bf16x2(r0, r1);
-                    }
-                }
-                lo[kb] = __builtin_bit_cast(bf16x8, lw);
-            }
+            for (int kb = 0; kb < 2; ++kb) lo[kb] = __builtin_bit_cast(bf16x8, lwv[h][kb]);
 #pragma unroll
             for (int t = 0; t < 8; ++t) Sc[h][t] = Sc[h][t] * gam;
 #pragma unroll
