@@ -374,6 +374,15 @@ def bench_twolevel(ops, dev, reps=10):
         ms_plain = time_calls(plain, 1, reps * 2, 3)
         nch = [(n + 63) // 64 for n in lens]
         seg_len = max(-(-c // min(segs, c)) if c else 0 for c in nch)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+        def groups(pairs):
+            # the library's scan instance: 16-column groups while they fit on
+            # the CUs at once, the paired 32-column instance beyond
+            per = 8 if pairs * 8 <= cus else 4
+            return -(-pairs // 8) * 8 * per
+
+        nseg = sum(min(segs, c) if c else 1 for c in nch)
         out[name] = {"us_plain": round(ms_plain * 1e3, 2),
                      "us_twolevel": round(sum(med), 2),
                      "us_prep": round(med[0], 2), "us_pass1_B": round(med[1], 2),
@@ -381,9 +390,8 @@ def bench_twolevel(ops, dev, reps=10):
                      "us_replay": round(med[4], 2),
                      "serial_chunks_plain": max(nch),
                      "serial_chunks_twolevel": 2 * seg_len + max(0, min(segs, max(nch)) - 2),
-                     "scan_groups_plain": -(-N * HV // 8) * 64,
-                     "scan_groups_per_pass_twolevel": -(-sum(min(segs, c) if c else 1
-                                                             for c in nch) * HV // 8) * 64}
+                     "scan_groups_plain": groups(N * HV),
+                     "scan_groups_per_pass_twolevel": groups(nseg * HV)}
         del ws, d
     return out
 
