@@ -947,7 +947,10 @@ __device__ __forceinline__ void lds_st(int* p, int v) {
 }
 
 // LDS store of a counter, invisible to the compiler's wait placement: use
-// only where an explicit s_waitcnt has already ordered what it publishes.
+// only where an explicit s_waitcnt has already ordered what it publishes, or
+// where what it publishes are this wave's earlier LDS writes (a wave's LDS
+// operations are performed in issue order) and reads whose values this wave
+// has already consumed.
 __device__ __forceinline__ void lds_st_asm(int* p, int v) {
     const uint32_t addr = (uint32_t)(size_t)(__attribute__((address_space(3))) int*)p;
     asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
@@ -1157,8 +1160,10 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
         load_t(c + 3, th, tl);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) st.U[mt][lane] = U[mt];
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.uready, c + 1);
+        // published behind the U writes (LDS operations are performed in
+        // issue order)
+        asm volatile("" ::: "memory");
+        if (lane == 0) lds_st_asm(&sm.uready, c + 1);
         return true;
     };
     if (x.nch <= 0) return;
@@ -1372,12 +1377,17 @@ __device__ void run_chain(ScanSmem& sm, const ScanArgs& a, const Waiter& w, cons
         sm.h[hs].V[0][lane] = vh[0];
         sm.h[hs].V[1][lane] = vh[1];
         __builtin_amdgcn_sched_barrier(0);
-        lds_wait_all();
+        // The counters go out behind this step's hand-off writes without
+        // waiting for them: a wave's LDS operations are performed in issue
+        // order, so a wave that sees a counter also sees what it publishes.
+        // The chain's reads of ring C and ring P have completed (the products
+        // consumed them), so freeC may release those stages.
+        asm volatile("" ::: "memory");
         if (lane == 0) {
-            lds_st(&sm.ready, c + 1);
-            lds_st(&sm.freeC, c + 1);
-            if (!kDbg) lds_st(&sm.dvready, c + 1);
-            else lds_st(&sm.kfree, c + 1);   // no helper: the chain read K^T
+            lds_st_asm(&sm.ready, c + 1);
+            lds_st_asm(&sm.freeC, c + 1);
+            if (!kDbg) lds_st_asm(&sm.dvready, c + 1);
+            else lds_st_asm(&sm.kfree, c + 1);   // no helper: the chain read K^T
         }
     }
     if (!ok) return;
@@ -1993,8 +2003,8 @@ __device__ void run_producer2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w,
         }
         // the products have read this set: chunk c + 2's fragments go in
         load_t(c + 2, th, tl);
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.uready, c + 1);
+        asm volatile("" ::: "memory");
+        if (lane == 0) lds_st_asm(&sm.uready, c + 1);
         return true;
     };
     if (x.nch <= 0) return;
@@ -2156,11 +2166,12 @@ __device__ void run_chain2(ScanSmem2& sm, const ScanArgs& a, const Waiter& w, co
         sm.h[hs].V[hh][0][lane] = vh[0];
         sm.h[hs].V[hh][1][lane] = vh[1];
         __builtin_amdgcn_sched_barrier(0);
-        lds_wait_all();
+        // published behind this step's LDS writes, as in the 16-column chain
+        asm volatile("" ::: "memory");
         if (lane == 0) {
-            lds_st(&sm.ready[hh], c + 1);
-            lds_st(&sm.freeC[hh], c + 1);
-            lds_st(&sm.dvready[hh], c + 1);
+            lds_st_asm(&sm.ready[hh], c + 1);
+            lds_st_asm(&sm.freeC[hh], c + 1);
+            lds_st_asm(&sm.dvready[hh], c + 1);
         }
     }
     if (!ok) return;
