@@ -158,6 +158,7 @@ def bench_prefill_norm(ops, dev, steps, warmup):
 
 
 def bench_varlen(ops, dev, steps, warmup):
+    import torch
     import gdn_cases as gc
 
     q, k, v, g, beta, s0, cu = gc.varlen_inputs()
@@ -167,7 +168,32 @@ def bench_varlen(ops, dev, steps, warmup):
     total = int(cu[-1])
     flops = gc.flops_prefill(total, v.shape[2])
     algo = _bytes(q, k, v, g, beta, s0) + _bytes(v) + _bytes(s0)
-    return dict(ms=ms, tflops=flops / ms / 1e9, gbs=algo / ms / 1e6, tokens=total)
+    out = dict(ms=ms, tflops=flops / ms / 1e9, gbs=algo / ms / 1e6, tokens=total)
+    # the same call with each scan instance forced (deltanet_chunk_prefill_cols):
+    # 16 value columns per work-group, and the paired 32 the library picks here
+    import ctypes as ct
+    from gdn_hip import capi
+
+    lib = capi.lib()
+    N, HV, HK = len(cu) - 1, v.shape[2], q.shape[2]
+    wsb = lib.deltanet_prefill_varlen_live_workspace_size(total, N, HV, 128, 128, 64)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    o = torch.empty_like(d[2])
+    sf = torch.empty(N, HV, 128, 128, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def forced(cols):
+        def call(i):
+            err = lib.deltanet_chunk_prefill_cols(
+                *[t.data_ptr() for t in d[:5]], o.data_ptr(), d[5].data_ptr(), sf.data_ptr(),
+                cud.data_ptr(), N, total, HV, HK, ws.data_ptr(), wsb, stream, cols, ct.c_uint(0))
+            assert err == 0, err
+        return time_calls(call, 1, steps, warmup)
+
+    out["ms_scan16"] = forced(16)
+    out["ms_scan32"] = forced(32)
+    del ws
+    return out
 
 
 def bench_decode(ops, dev, steps, warmup):
@@ -787,7 +813,9 @@ def main():
                 "nontemporal": sp[1]["nontemporal"], "blocks_per_cu": sp[1]["blocks_per_cu"]},
             "varlen_prefill_8seq_19861tok": {"us": round(var["ms"] * 1e3, 2),
                                   "TFLOP/s": round(var["tflops"], 3),
-                                  "tokens": var["tokens"]},
+                                  "tokens": var["tokens"],
+                                  "us_scan_16col_forced": round(var["ms_scan16"] * 1e3, 2),
+                                  "us_scan_32col_forced": round(var["ms_scan32"] * 1e3, 2)},
             "causal_conv1d_silu_1141x8192_k4": {"us": round(cv["ms"] * 1e3, 2),
                                                 "GB/s": round(cv["gbs"], 1),
                                                 "hbm_frac": round(cv["frac"], 4)},
