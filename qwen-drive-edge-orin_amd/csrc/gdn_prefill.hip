@@ -155,6 +155,7 @@ struct PrepIn {
     const uint16_t* b;
     const float* A_log;
     const uint16_t* dt_bias;
+    const float* s0;   // the scan's initial state (the prep only touches it)
 };
 
 // ---------------------------------------------------------------------------
@@ -451,7 +452,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     PrepIn in, const int32_t* __restrict__ cu, int N, int T, int total, int HV, int HK,
     int nch_bound, float scale, Workspace ws) {
     __shared__ PrepSmem sm;
-    // The kernel arguments (232 bytes) span four 64-byte lines, which the
+    // The kernel arguments (240 bytes) span four 64-byte lines, which the
     // scalar cache would otherwise fetch in three dependent round trips (each
     // use waits before the branch that leads to the next): fields at most 32
     // bytes apart, all requested together, cost one.
@@ -482,7 +483,6 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     if (!locate_chunk<kPrepThreads>(cu, N, T, total, cid, reinterpret_cast<int*>(sm.AT), seq,
                                     tok0, rows))
         return;
-    (void)seq;
     const size_t ch = (size_t)cid * HV + hv;
     // this call's gated-RMSNorm slots start invalid (2 KB: 16 bytes a
     // thread; only when the scan runs the norm epilogue)
@@ -525,6 +525,18 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             q + ((size_t)(tok0 + min(wave * 16 + lm, rows - 1)) * HK + hk) * kDK + 8 * lg;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) qr[kb] = *reinterpret_cast<const u32x4*>(qs + kb * 32);
+    }
+    // The scan's first step waits on the initial state; read cold from HBM
+    // that costs it ~2 us.  Each group here reads a 4 KB share of its
+    // (sequence, v-head) state (chunk cs of the sequence: bytes [4 cs, 4 cs
+    // + 4) KB, so 16 chunks cover the 64 KB), which leaves it in the
+    // memory-side cache for the scan; the values are discarded.
+    u32x4 ts0 = u32x4{0u, 0u, 0u, 0u};
+    if (in.s0) {
+        const int cs = (tok0 - seq_lo(cu, T, total, seq)) / kChunk;
+        const size_t off = (size_t)cs * (kPrepThreads * 4) + 4 * tid;
+        if (off < (size_t)kDK * kDV)
+            ts0 = *reinterpret_cast<const u32x4*>(in.s0 + ((size_t)seq * HV + hv) * kDK * kDV + off);
     }
     // the gate arithmetic (and so the wait for its inputs) stays behind the
     // K and Q loads
@@ -619,6 +631,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         st_through(&gr[kGC63 + lane], lane == 0 ? c63 : 0.f);
         if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
     }
+    asm volatile("" ::"v"(ts0));   // the share is read (and waited for) before the products
     __syncthreads();
 
     // ---- A = -beta_r (k_r . k_j) Gamma_rj (r > j) and M = s (q_r . k_j) Gamma_rj (r >= j)
@@ -1754,7 +1767,7 @@ __device__ inline void scan_context(const ScanArgs& a, int pidx, int* seqsel, in
 template <int kRaw, bool kDbg, bool kNorm = false>
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     __shared__ ScanSmem sm;
-    // The kernel arguments (280 bytes) span five 64-byte lines, which the
+    // The kernel arguments (288 bytes) span five 64-byte lines, which the
     // scalar cache would otherwise fetch in three dependent round trips:
     // fields at most 32 bytes apart, all requested together, cost one.
     asm volatile("" ::"s"(a.in.q), "s"(a.in.beta), "s"(a.in.dt_bias), "s"(a.ws.M), "s"(a.ws.KT),
@@ -2483,7 +2496,9 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
         auto kern = raw == 1 ? gdn_prep_kernel<false, 1>
                     : raw == 2 ? gdn_prep_kernel<false, 2>
                     : dump_debug ? gdn_prep_kernel<true, 0> : gdn_prep_kernel<false, 0>;
-        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kPrepThreads), 0, stream, in, cu, N, T,
+        PrepIn pin = in;
+        pin.s0 = s0;
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kPrepThreads), 0, stream, pin, cu, N, T,
                            total_tokens, HV, HK, (int)nch_bound, scale, ws);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
