@@ -58,14 +58,37 @@ def whole_call_roofline(flops, algo_bytes, ms):
             "frac_of_attainable": round(tflops / attain, 4)}
 
 
-def time_calls(fn, n_sets, steps, warmup):
-    """HIP-event time of `steps` back-to-back calls fn(i) on the current
-    stream, bracketed by device synchronisation; returns ms per call."""
+# Untimed warm-up before every timed region lasts at least this long: from an
+# idle GPU the first ~10 ms of back-to-back calls run several percent slower
+# (the T=1141 prefill measured 41.5 us per call over its first 220 calls
+# against 38.3 us after).
+WARM_S = 0.05
+
+
+def warm_up(fn, n_sets, warmup):
+    """`warmup` untimed calls, then more in batches until WARM_S seconds of
+    device-synchronised calls have passed."""
+    import time
     import torch
 
-    for i in range(warmup):
-        fn(i % n_sets)
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        for _ in range(max(warmup, 1)):
+            fn(i % n_sets)
+            i += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= WARM_S:
+            return
+
+
+def time_calls(fn, n_sets, steps, warmup):
+    """HIP-event time of `steps` back-to-back calls fn(i) on the current
+    stream, bracketed by device synchronisation, after warm_up; returns ms
+    per call."""
+    import torch
+
+    warm_up(fn, n_sets, warmup)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -94,8 +117,7 @@ def time_graph(fn, n_sets, reps, warmup):
             for i in range(n_sets):
                 fn(i)
     torch.cuda.current_stream().wait_stream(stream)
-    graph.replay()
-    torch.cuda.synchronize()
+    warm_up(lambda i: graph.replay(), 1, 1)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -545,9 +567,7 @@ def kernel_times(dev, steps, warmup):
         if j > 0:
             for i in range(len(sets)):
                 launch(i, -1)   # every workspace holds its inputs' records
-        for i in range(warmup):
-            launch(i, j)
-        torch.cuda.synchronize()
+        warm_up(lambda i: launch(i, j), len(sets), warmup)
         ev = hip.events(2)
         hip.record(ev[0], stream)
         for i in range(steps):
