@@ -83,17 +83,21 @@ def test_pair_equals_16col_edges(lib, dev):
     _same(lib, dev, [t.to(dev) for t in (q, k, v, g, beta, s0)], cu, "varlen edges")
 
 
-@pytest.mark.parametrize("HK,HV", [(2, 4), (16, 16)])
-def test_pair_equals_16col_batch_head_maps(lib, dev, HK, HV):
-    """Fixed-length batches, no initial state cleared: GQA 2 and 1."""
-    d = [t.to(dev) for t in gc.make_gdn_inputs(61 + HV, B=3, T=300, HK=HK, HV=HV, g_shift=2.0)]
-    _same(lib, dev, d, None, f"B3 T300 HK{HK} HV{HV}")
+@pytest.mark.parametrize("B,T,HK,HV", [(3, 300, 2, 4), (3, 300, 16, 16), (3, 200, 4, 12),
+                                       (40, 100, 1, 1)])
+def test_pair_equals_16col_batch_head_maps(lib, dev, B, T, HK, HV):
+    """Fixed-length batches: GQA 2, 1 and 3, a head count that is not a
+    multiple of 8 (HV=12: partial XCD rows of the group-id map), and 40
+    one-head sequences (the library picks the paired instance there)."""
+    d = [t.to(dev) for t in gc.make_gdn_inputs(61 + HV + B, B=B, T=T, HK=HK, HV=HV, g_shift=2.0)]
+    _same(lib, dev, d, None, f"B{B} T{T} HK{HK} HV{HV}")
 
 
 def test_pair_spin_limit_reports_timeout(lib, dev):
-    """The paired instance's waits limited to zero polls give up at once:
-    every kernel returns normally and the status word reports
-    hipErrorLaunchTimeOut; a normal call on fresh buffers succeeds."""
+    """The paired instance's waits limited to one poll (spin_limit 0 would
+    mean the library's own limit here) give up at once: every kernel returns
+    normally and the status word reports hipErrorLaunchTimeOut; a normal
+    call on fresh buffers succeeds."""
     q, k, v, g, beta, s0, cu = gc.varlen_inputs(torch.tensor([300, 200, 64]))
     d = [t.to(dev) for t in (q, k, v, g, beta, s0)]
     _, _, st = _run(lib, dev, d, cu, 32, spin=1)
