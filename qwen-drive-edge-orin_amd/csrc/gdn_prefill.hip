@@ -1740,6 +1740,14 @@ __device__ inline void scan_context(const ScanArgs& a, int pidx, int* seqsel, in
     const int tid = threadIdx.x;
     x.seq = pidx / a.HV;
     x.hv = pidx - x.seq * a.HV;
+    // pidx % 8 is the XCD: give the v-heads of one k-head the same XCD (one
+    // L2 then holds that k-head's K^T and Q records for all of them) when
+    // the heads tile the 8 XCDs evenly
+    const int rep = a.HV / a.HK;
+    if (rep > 1 && a.HV % 8 == 0 && a.HK % 8 == 0) {
+        const int r = x.hv >> 3, xcd = x.hv & 7;
+        x.hv = (xcd + 8 * (r / rep)) * rep + r % rep;
+    }
     if (a.cu && a.N <= kScanThreads) {
         if (tid < a.N) {
             const int my = seq_count(a.cu, a.T, a.total, tid);
@@ -1777,7 +1785,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
 
     // XCD-aware id: the eight groups of one (sequence, head) share id % 8
-    // (one XCD, one L2), so their K, -W, Q and M come from one L2
+    // (one XCD, one L2), so their K, -W, Q and M come from one L2, and so
+    // do the heads of one k-head where scan_context can arrange it
     const int id = blockIdx.x;
     const int xcd = id & 7, qd = id >> 3;
     ScanCtx x;
