@@ -80,11 +80,13 @@ def _check(o, o_ref, s, s_ref, tag):
 
 
 @pytest.mark.parametrize("B,T,HK,HV", [(1, 150, 2, 4), (2, 64, 1, 2), (1, 1141, 2, 4),
-                                       (1, 1141, 16, 32)])
+                                       (1, 1141, 16, 32), (2, 300, 16, 32)])
 def test_chunk_matches_transformers(fla_ops, torch_ref, dev, B, T, HK, HV):
     """(1, 1141, 16, 32) is the planner's layer: 16 k-heads expanded to the 32
     v-heads before the call (modeling_qwen3_5.py:500-502), as transformers
-    hands them to fla."""
+    hands them to fla.  (2, 300, 16, 32) has more (sequence, head) pairs than
+    one 16-column scan group per CU covers, so it runs the paired scan's
+    raw-bf16 instance."""
     q, k, v, g, beta, s0 = _layer_inputs(B, T, HK, HV, seed=T + HV)
     o_ref, s_ref = torch_ref[0](q.float(), k.float(), v.float(), g, beta, initial_state=s0,
                                 output_final_state=True, use_qk_l2norm_in_kernel=True)

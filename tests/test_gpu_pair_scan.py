@@ -118,3 +118,28 @@ def test_cols_rejects(lib, dev):
             capi.ptr(q), capi.ptr(k), capi.ptr(v), capi.ptr(g), capi.ptr(beta), o.data_ptr(),
             s0.data_ptr(), sf.data_ptr(), None, 1, 64, 4, 2, ws.data_ptr(), wsb, _stream(), cols,
             ct.c_uint(0)) == capi.HIP_ERROR_INVALID_VALUE
+
+
+def test_pair_noalloc_matches_workspace_entry(lib, dev):
+    """The allocation-free entry at a shape where the library picks the
+    paired scan (B=2 T=300 HV=32: 320 chunk-heads, inside its array) gives
+    bitwise the workspace entry's o and final state, and reports success."""
+    q, k, v, g, beta, s0 = [t.to(dev) for t in gc.make_gdn_inputs(71, B=2, T=300, HK=16, HV=32,
+                                                                   g_shift=2.0)]
+    B, T, HK, D = q.shape
+    HV = v.shape[2]
+    wsb = lib.deltanet_prefill_live_workspace_size(B, T, HV, D, D, 64)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    o1, o2 = torch.empty_like(v), torch.empty_like(v)
+    s1, s2 = torch.empty_like(s0), torch.empty_like(s0)
+    args = [capi.ptr(t) for t in (q, k, v, g, beta)]
+    print(f"[pair] noalloc B={B} T={T} HV={HV}", flush=True)
+    assert lib.deltanet_chunk_prefill(*args, o1.data_ptr(), s0.data_ptr(), s1.data_ptr(), B, T,
+                                      HV, HK, D, D, 64, ws.data_ptr(), wsb, _stream(),
+                                      0) == capi.HIP_SUCCESS
+    assert lib.deltanet_chunk_prefill_noalloc(*args, o2.data_ptr(), s0.data_ptr(), s2.data_ptr(),
+                                              B, T, HV, HK, D, D, 64,
+                                              _stream()) == capi.HIP_SUCCESS
+    assert lib.deltanet_prefill_noalloc_status(_stream()) == capi.HIP_SUCCESS
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
