@@ -35,7 +35,10 @@
 //         direct-to-LDS loads; a norm wave serves the gated-RMSNorm epilogue.
 //         Waves meet through LDS counters with bounded waits; a wait that runs
 //         out aborts the work-group and sets the workspace's status word
-//         (deltanet_prefill_status).
+//         (deltanet_prefill_status).  Once a call's 16-column groups would
+//         outnumber the CUs, a paired instance gives each work-group 32
+//         columns as two 16-column halves sharing the chunk operands
+//         (gdn_scan2_kernel; bitwise the same results).
 //
 // Rounding budget (checked against an fp64 emulation of each operand class):
 // W and S rounded to fp16 for V_n change the final state by < 1e-4 relative;
