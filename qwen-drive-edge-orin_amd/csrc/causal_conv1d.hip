@@ -28,7 +28,8 @@ namespace gdn {
 namespace {
 
 constexpr int kConvThreads = 256;
-constexpr int kConvMaxRun = 12;     // longest token run of one work-group
+constexpr int kConvMaxRun = 12;     // longest token run of the many-rounds launch
+constexpr int kConvFastMax = 24;    // longest token run of the one-or-two-rounds launch
 constexpr int kConvMaxState = 8;    // longest carried state of the update
 
 // element loads / stores by dtype code (0 bf16, 1 fp16, 2 fp32)
@@ -126,10 +127,23 @@ __device__ inline u32x4 finish8(const float (&acc)[8]) {
 }
 
 // Work units: (batch, token run, channel tile of 2048) with the channel tile
-// fastest.  The launcher sizes the runs (at most kConvMaxRun tokens, equal
-// lengths but the last) so the grid holds about two waves per SIMD: every
-// SIMD then gets the same number of equal waves, where fixed short tiles
-// leave some SIMDs one wave more than others.  Work-groups are dealt
+// fastest; runs have equal lengths but the last.  Two launch regimes:
+//  - one or two rounds: when runs of at most kConvFastMax tokens can cover
+//    the input with at most one (else two) work-groups per CU, the run is
+//    sized so they do, and the instance's slot count kMaxRun is the
+//    smallest of kFastRuns that holds it.  Each wave then issues all its
+//    rows at once and turns them into outputs as they arrive, with no
+//    second round to wait for; the x rows are read non-temporally.
+//  - many rounds: otherwise runs of at most kConvMaxRun tokens, sized for
+//    about two waves per SIMD, in the 12-slot instance.
+// Measured at D = 8192, K = 4, bf16 with SiLU (graph-replayed over rotated
+// copies): T = 1141 takes 9.2 us in one round of 18-token runs against 10.7
+// us with 9-token runs over two waves per SIMD, and 0.84-0.97x of that time
+// from T = 64 to 3000; past that (T = 4096: 31.8 us) the many-rounds form is
+// as fast as any run length.  A slot past the run re-reads the run's last
+// row, which a non-temporal load takes from HBM again: 18-token runs in the
+// 24-slot instance took 10.4 us, hence the close-fitting slot counts.
+// Work-groups are dealt
 // round-robin to the 8 XCDs (each with its own L2); remapping the
 // work-group id gives every XCD one contiguous range of units, so the K-1
 // halo rows a run shares with the previous run are read from the same L2.
@@ -138,7 +152,7 @@ __device__ inline int xcd_unit(int id, int n) {
     return xcd * q + min(xcd, r) + id / 8;
 }
 
-template <int IO, int WT, int K, bool SILU, bool BIAS>
+template <int IO, int WT, int K, bool SILU, bool BIAS, int kMaxRun, bool kNT>
 __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const void* __restrict__ bias,
     uint16_t* __restrict__ y, int T, int D, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
@@ -164,13 +178,15 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
         if constexpr (BIAS) bf[e] = ld_elem<WT>(bias, d0 + e);
     }
     // then all rows t0-K+1 .. t0+len-1; rows before 0 are zero, the slots
-    // past the run re-read its last row (a cache hit)
-    constexpr int kRows = kConvMaxRun + K - 1;
+    // past the run re-read its last row
+    constexpr int kRows = kMaxRun + K - 1;
     u32x4 raw[kRows];
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
         const int tc = min(max(t0 - (K - 1) + i, 0), t0 + len - 1);
-        raw[i] = *reinterpret_cast<const u32x4*>(xb + (size_t)tc * xts);   // cached: halo rows
+        const u32x4* p = reinterpret_cast<const u32x4*>(xb + (size_t)tc * xts);
+        if constexpr (kNT) raw[i] = __builtin_nontemporal_load(p);
+        else raw[i] = *p;   // cached: the K-1 halo rows come from L2
     }
     // every load is issued before any is waited for: the scheduler would
     // otherwise hold back later rows behind the first rows' use
@@ -193,7 +209,7 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
     // compiler sink its load into that block, where it is issued late and
     // waited for at once.
 #pragma unroll
-    for (int i = 0; i < kConvMaxRun; ++i) {
+    for (int i = 0; i < kMaxRun; ++i) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             win[K - 1][2 * p] = lo16<IO>(raw[i + K - 1][p]);
@@ -438,15 +454,51 @@ int device_cus() {
     return n;
 }
 
+// Run length of the one-or-two-rounds launch (at most kConvFastMax tokens,
+// the grid at most `rounds` work-groups per CU), or 0 where it needs more.
+int fast_run(int T, int64_t per_row, int cus) {
+    for (int rounds = 1; rounds <= 2; ++rounds) {
+        const int64_t n_runs = (int64_t)rounds * cus / per_row;
+        if (n_runs < 1) continue;
+        const int64_t run = (T + n_runs - 1) / n_runs;
+        if (run <= kConvFastMax) return (int)run;
+    }
+    return 0;
+}
+
 template <int IO, int WT, bool SILU, bool BIAS>
 hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, int B, int T, int D,
                       int K, int64_t xbs, int64_t xts, int64_t ybs, int64_t yts,
                       hipStream_t stream) {
     const int n_ctiles = (D / 8 + kConvThreads - 1) / kConvThreads;
-    // about two waves per SIMD (2 work-groups of 4 waves per CU), runs of
-    // equal length up to kConvMaxRun tokens
     const int cus = device_cus();
     const int64_t per_row = (int64_t)B * n_ctiles;
+    auto xp = static_cast<const uint16_t*>(x);
+    auto yp = static_cast<uint16_t*>(y);
+    // one or two rounds: the transformers case (K = 4, weights in the I/O
+    // dtype), slot counts 1..24 with at most one slot past the run
+    if constexpr (IO == WT) {
+        const int run = K == 4 ? fast_run(T, per_row, cus) : 0;
+        if (run > 0) {
+            const int n_runs = (T + run - 1) / run;
+            const dim3 grid((unsigned)(per_row * n_runs));   // <= 2 x CUs
+#define GDN_CONV_FAST(R)                                                                       \
+    if (run <= R) {                                                                            \
+        hipLaunchKernelGGL((causal_conv1d_fwd_kernel<IO, WT, 4, SILU, BIAS, R, true>), grid,    \
+                           dim3(kConvThreads), 0, stream, xp, w, bias, yp, T, D, xbs, xts, ybs, \
+                           yts, n_ctiles, n_runs, run);                                        \
+        return hipGetLastError();                                                              \
+    }
+            GDN_CONV_FAST(1) GDN_CONV_FAST(2) GDN_CONV_FAST(3) GDN_CONV_FAST(4)
+            GDN_CONV_FAST(6) GDN_CONV_FAST(8) GDN_CONV_FAST(10) GDN_CONV_FAST(12)
+            GDN_CONV_FAST(14) GDN_CONV_FAST(16) GDN_CONV_FAST(18) GDN_CONV_FAST(20)
+            GDN_CONV_FAST(22) GDN_CONV_FAST(24)
+#undef GDN_CONV_FAST
+            static_assert(kConvFastMax == 24, "the slot counts above end at kConvFastMax");
+        }
+    }
+    // many rounds: about two waves per SIMD (2 work-groups of 4 waves per
+    // CU), runs of equal length up to kConvMaxRun tokens
     int64_t n_runs = (2LL * cus + per_row / 2) / per_row;
     n_runs = std::max<int64_t>(1, std::min<int64_t>(n_runs, T));
     int run = (int)((T + n_runs - 1) / n_runs);
@@ -455,13 +507,12 @@ hipError_t launch_fwd(const void* x, const void* w, const void* bias, void* y, i
     const int64_t units = per_row * n_runs;
     if (units > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 grid((unsigned)units);
-    auto xp = static_cast<const uint16_t*>(x);
-    auto yp = static_cast<uint16_t*>(y);
 #define GDN_CONV_FWD(KK)                                                                       \
     case KK:                                                                                   \
-        hipLaunchKernelGGL((causal_conv1d_fwd_kernel<IO, WT, KK, SILU, BIAS>), grid,          \
-                           dim3(kConvThreads), 0, stream, xp, w, bias, yp, T, D, xbs, xts, ybs, \
-                           yts, n_ctiles, (int)n_runs, run);                                   \
+        hipLaunchKernelGGL((causal_conv1d_fwd_kernel<IO, WT, KK, SILU, BIAS, kConvMaxRun,      \
+                                                     false>),                                  \
+                           grid, dim3(kConvThreads), 0, stream, xp, w, bias, yp, T, D, xbs,    \
+                           xts, ybs, yts, n_ctiles, (int)n_runs, run);                         \
         break;
     switch (K) {
         GDN_CONV_FWD(2)

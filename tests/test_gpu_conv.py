@@ -66,6 +66,44 @@ def test_fwd_qwen_shape(ops, dev, T):
     _check(y, ref, "silu", f"fwd T={T}")
 
 
+# Lengths at D = 8192 (4 channel tiles) that give, on a 256-CU device, runs
+# of ceil(T / 64) tokens in one round up to T = 1536 (40 .. 1500: runs 1, 2,
+# 3, 4, 5, 6, 8, 10, 11, 15, 18, 20, 21, 24, i.e. every slot count of that
+# launch, with and without a slot past the run), ceil(T / 128) in two rounds
+# up to 3072 (1600, 2048, 3000) and the many-rounds launch past that (3100).
+RUN_LENGTHS = [40, 100, 150, 250, 300, 380, 500, 600, 700, 900, 1141, 1250, 1300, 1500, 1600,
+               2048, 3000, 3100]
+
+
+@pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
+def test_fwd_run_lengths(ops, dev, io):
+    """Every launch shape of the K = 4 prefill at the Qwen3.5 width: without
+    activation bit-identical to the oracle, with a bias; with SiLU at the
+    tolerance above."""
+    for T in RUN_LENGTHS:
+        x, w, bias = _inputs(T + 1, 1, T, D_QWEN, 4, io, io)
+        xd, wd_, bd = x.to(dev), w.to(dev), bias.to(dev)
+        print(f"fwd run lengths T={T} {io}", flush=True)
+        y = ops.causal_conv1d_fwd(xd, wd_, bd, False)
+        torch.cuda.synchronize()
+        _check(y, orc.causal_conv1d(x, w, bias, None), None, f"fwd T={T} {io} bias")
+        y = ops.causal_conv1d_fwd(xd, wd_, None, True)
+        torch.cuda.synchronize()
+        _check(y, orc.causal_conv1d(x, w, None, "silu"), "silu", f"fwd T={T} {io} silu")
+
+
+def test_fwd_run_lengths_batch_and_partial_tile(ops, dev):
+    """Batches (B = 2, 5) and a width with a partial last channel tile
+    (D = 2048 + 264), so that runs, batches and channel tiles share the
+    grid, bit-identical to the oracle."""
+    for B, T, D in [(2, 1141, D_QWEN), (5, 300, D_QWEN), (3, 700, 2312), (2, 2000, 2312)]:
+        x, w, bias = _inputs(B * T, B, T, D, 4, torch.bfloat16, torch.bfloat16)
+        print(f"fwd B={B} T={T} D={D}", flush=True)
+        y = ops.causal_conv1d_fwd(x.to(dev), w.to(dev), bias.to(dev), False)
+        torch.cuda.synchronize()
+        _check(y, orc.causal_conv1d(x, w, bias, None), None, f"fwd B={B} T={T} D={D}")
+
+
 @pytest.mark.parametrize("io,wd", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                    (torch.bfloat16, torch.float32), (torch.float16, torch.float32)])
 @pytest.mark.parametrize("K", [2, 3, 4])
