@@ -130,23 +130,24 @@ __device__ inline u32x4 finish8(const float (&acc)[8]) {
 // fastest; runs have equal lengths but the last.  Two launch regimes:
 //  - one or two rounds: when runs of at most kConvFastMax tokens can cover
 //    the input with at most one (else two) work-groups per CU, the run is
-//    sized so they do, and the instance's slot count kMaxRun is the
-//    smallest of kFastRuns that holds it.  Each wave then issues all its
-//    rows at once and turns them into outputs as they arrive, with no
-//    second round to wait for; the x rows are read non-temporally.
+//    sized so they do, in the instance with the smallest slot count kMaxRun
+//    (1-4, 6, 8, ..., 24) that holds it.  Each wave issues all its rows at
+//    once and turns them into outputs as they arrive, with no second round
+//    to wait for; the x rows are read non-temporally.
 //  - many rounds: otherwise runs of at most kConvMaxRun tokens, sized for
 //    about two waves per SIMD, in the 12-slot instance.
 // Measured at D = 8192, K = 4, bf16 with SiLU (graph-replayed over rotated
 // copies): T = 1141 takes 9.2 us in one round of 18-token runs against 10.7
-// us with 9-token runs over two waves per SIMD, and 0.84-0.97x of that time
-// from T = 64 to 3000; past that (T = 4096: 31.8 us) the many-rounds form is
-// as fast as any run length.  A slot past the run re-reads the run's last
-// row, which a non-temporal load takes from HBM again: 18-token runs in the
-// 24-slot instance took 10.4 us, hence the close-fitting slot counts.
-// Work-groups are dealt
-// round-robin to the 8 XCDs (each with its own L2); remapping the
-// work-group id gives every XCD one contiguous range of units, so the K-1
-// halo rows a run shares with the previous run are read from the same L2.
+// us with 9-token runs over two waves per SIMD, and 0.84-0.97x of the
+// many-rounds time from T = 64 to 3000; past that (T = 4096: 31.8 us) the
+// many-rounds form is as fast as any run length.  A slot past the run
+// re-reads the run's last row, which a non-temporal load takes from HBM
+// again: 18-token runs in the 24-slot instance took 10.4 us, hence the
+// close-fitting slot counts.
+// Work-groups are dealt round-robin to the 8 XCDs (each with its own L2);
+// remapping the work-group id gives every XCD one contiguous range of units,
+// so the K-1 halo rows a run shares with the previous run are read from the
+// same L2.
 __device__ inline int xcd_unit(int id, int n) {
     const int q = n / 8, r = n % 8, xcd = id % 8;
     return xcd * q + min(xcd, r) + id / 8;
