@@ -1,20 +1,27 @@
 """Seeded random shapes against the CPU oracle: the chunked prefill (fixed
 length and packed batches, GQA ratios 1/2/4, with and without an initial
-state, so that both scan instances and every chunk-tail case come up) and the
-causal conv1d prefill (widths with partial channel tiles, K = 2..4, both I/O
-dtypes, bias, both launch regimes).  The cases are drawn once from a fixed
-seed; each prints its shape before it runs.
+state, so that both scan instances and every chunk-tail case come up), the
+recurrent decode step (batch, tokens per call, GQA ratio, state scale and
+gate range), the causal conv1d prefill (widths with partial channel tiles,
+K = 2..4, both I/O dtypes, bias, both launch regimes), the conv1d decode
+update (the 4-channel vector path and the per-channel path: state lengths
+K-1..8, several tokens per call) and the gated RMSNorm (row counts, head
+widths, dtypes, fp32 or I/O-dtype weights).  The cases are drawn once from a
+fixed seed; each prints its shape before it runs.
 
-Bars as in test_gpu_prefill.py (max |err| <= 2e-2 on o and the final state,
-the reference harness's random-case bar) and test_gpu_conv.py (bit-identical
-without activation; with SiLU every element within 1 ulp and at most 1e-3 of
-them different).
+Bars as in test_gpu_prefill.py and test_gpu_decode_norm.py (max |err| <= 2e-2
+on o and the final state, the reference harness's random-case bar; the
+RMSNorm within one rounding step per stage, >= 99.9 % bitwise) and
+test_gpu_conv.py (bit-identical without activation; with SiLU every element
+within 1 ulp and at most 1e-3 of them different; the carried state
+bit-identical).
 """
 import pytest
 import torch
 
 import gdn_cases as gc
 from oracle import gdn_oracle as orc
+from test_gpu_decode_norm import _decode_check, _norm_check
 
 pytestmark = pytest.mark.gpu
 
@@ -124,3 +131,107 @@ def test_conv_random_shape(ops, dev, case):
     n_diff = (y != ref).sum().item()
     assert _ulps(y, ref, io).max().item() <= 1.0
     assert n_diff <= 1e-3 * ref.numel(), n_diff
+
+
+def _decode_cases(n=8, seed=4242):
+    gen = torch.Generator().manual_seed(seed)
+
+    def pick(seq):
+        return seq[int(torch.randint(len(seq), (1,), generator=gen))]
+
+    cases = []
+    for i in range(n):
+        hk = pick([1, 2, 4, 8, 16])
+        hv = min(hk * pick([1, 2, 4]), 32)
+        hv -= hv % hk
+        cases.append(dict(seed=500 + i, B=int(torch.randint(1, 41, (1,), generator=gen)),
+                          T=int(torch.randint(1, 9, (1,), generator=gen)), hk=hk, hv=hv,
+                          s0_scale=pick([0.02, 0.5]), g_offset=pick([0.0, -1.0]),
+                          g_shift=pick([0.0, 2.0])))
+    return cases
+
+
+DECODE_CASES = _decode_cases()
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[f"d{i}" for i in range(len(DECODE_CASES))])
+def test_decode_random_shape(ops, dev, case):
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(case["seed"], B=case["B"], T=case["T"],
+                                              HK=case["hk"], HV=case["hv"],
+                                              g_shift=case["g_shift"], g_offset=case["g_offset"],
+                                              s0_scale=case["s0_scale"])
+    _decode_check(ops, dev, q, k, v, g, beta, s0,
+                  tag=f"random B={case['B']} T={case['T']} HK={case['hk']} HV={case['hv']} "
+                      f"s0={case['s0_scale']} g_off={case['g_offset']} g_shift={case['g_shift']}")
+
+
+def _update_cases(n=10, seed=91):
+    gen = torch.Generator().manual_seed(seed)
+
+    def pick(seq):
+        return seq[int(torch.randint(len(seq), (1,), generator=gen))]
+
+    cases = []
+    for i in range(n):
+        K = pick([2, 3, 4])
+        # every other case on the vector path's shape (K = 4, 4-token state)
+        L = 4 if i % 2 == 0 else int(torch.randint(K - 1, 9, (1,), generator=gen))
+        cases.append(dict(seed=700 + i, B=int(torch.randint(1, 71, (1,), generator=gen)),
+                          T=int(torch.randint(1, 5, (1,), generator=gen)),
+                          D=pick([264, 1032, 2312, 8192]), K=4 if i % 2 == 0 else K, L=L,
+                          io=pick([torch.bfloat16, torch.float16]), bias=pick([True, False])))
+    return cases
+
+
+UPDATE_CASES = _update_cases()
+
+
+@pytest.mark.parametrize("case", UPDATE_CASES, ids=[f"u{i}" for i in range(len(UPDATE_CASES))])
+def test_conv_update_random_shape(ops, dev, case):
+    B, T, D, K, L, io = case["B"], case["T"], case["D"], case["K"], case["L"], case["io"]
+    gen = torch.Generator().manual_seed(case["seed"])
+    x = torch.randn(B, T, D, generator=gen).to(io).transpose(1, 2)   # transformers' view
+    st = torch.randn(B, D, L, generator=gen).to(io)
+    w = (0.5 * torch.randn(D, K, generator=gen)).to(io)
+    bias = (0.1 * torch.randn(D, generator=gen)).to(io) if case["bias"] else None
+    print(f"[random conv update] B={B} T={T} D={D} K={K} L={L} {io} bias={case['bias']}",
+          flush=True)
+    for act in (None, "silu"):
+        ref, ref_st = orc.causal_conv1d_update(x, st, w, bias, act)
+        st_d = st.to(dev)
+        y = ops.causal_conv1d_update(x.to(dev), st_d, w.to(dev),
+                                     bias.to(dev) if bias is not None else None, act is not None)
+        torch.cuda.synchronize()
+        y = y.cpu()
+        assert torch.equal(st_d.cpu(), ref_st)
+        if act is None:
+            assert torch.equal(y, ref)
+        else:
+            assert _ulps(y, ref, io).max().item() <= 1.0
+            assert (y != ref).sum().item() <= max(1, 1e-3 * ref.numel())
+
+
+def _norm_cases(n=6, seed=313):
+    gen = torch.Generator().manual_seed(seed)
+
+    def pick(seq):
+        return seq[int(torch.randint(len(seq), (1,), generator=gen))]
+
+    return [dict(seed=900 + i, rows=int(torch.randint(1, 3000, (1,), generator=gen)),
+                 heads=int(torch.randint(1, 9, (1,), generator=gen)), dv=pick([64, 128, 256, 512]),
+                 io=pick([torch.bfloat16, torch.float16]), wdt=pick(["io", "fp32"]))
+            for i in range(n)]
+
+
+NORM_CASES = _norm_cases()
+
+
+@pytest.mark.parametrize("case", NORM_CASES, ids=[f"n{i}" for i in range(len(NORM_CASES))])
+def test_gated_rmsnorm_random_shape(ops, dev, case):
+    gen = torch.Generator().manual_seed(case["seed"])
+    shape = (case["rows"], case["heads"], case["dv"])
+    x = torch.randn(*shape, generator=gen).to(case["io"])
+    z = torch.randn(*shape, generator=gen).to(case["io"])
+    w = 1 + 0.1 * torch.randn(case["dv"], generator=gen)
+    w = w.to(case["io"]) if case["wdt"] == "io" else w
+    _norm_check(ops, dev, x, z, w, 1e-6, tag=f"random {shape} w={case['wdt']}")
