@@ -1135,7 +1135,7 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
             l[f] = pl[f * 64];
         }
     };
-    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri]) -> bool {
+    auto step = [&](int c, half8 (&th)[kTri], half8 (&tl)[kTri], bool refill = true) -> bool {
         // ring P of chunk c landed with loader group c - kLeadP (pfill); chunk
         // 0's, issued before loader 0's first ring-C stage, with that (fill)
         const int lc = c - kLeadP;
@@ -1176,7 +1176,7 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
             }
         }
         // the products have read this set: chunk c + 3's fragments go in
-        load_t(c + 3, th, tl);
+        if (refill) load_t(c + 3, th, tl);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) st.U[mt][lane] = U[mt];
         // published behind the U writes (LDS operations are performed in
@@ -1188,20 +1188,27 @@ __device__ void run_producer(ScanSmem& sm, const ScanArgs& a, const Waiter& w, c
     if (x.nch <= 0) return;
     half8 t0h[kTri], t0l[kTri], t1h[kTri], t1l[kTri], t2h[kTri], t2l[kTri];
     load_t(0, t0h, t0l);
+    load_t(1, t1h, t1l);
     // Start-up order: every group asks for its first records at once, so
-    // what the first chain step needs (ring C and P of chunk 0, T - I of
-    // chunk 0, the initial state) goes out first; loader 1's chunk 1, the
-    // T - I sets of chunks 1 and 2 and the output waves' Q and M wait until
-    // chunk 0 has landed (-0.3 us on the cold T=1141 HV=32 call)
+    // what the first chain steps need (ring C and P of chunk 0, T - I of
+    // chunks 0 and 1, the initial state) goes out first; loader 1's chunk 1
+    // and the output waves' Q and M wait until chunk 0 has landed (-0.3 us
+    // on the cold T=1141 HV=32 call).
     if (!w.until([&] { return lds_ld(&sm.fill[0]) >= 1; })) return;
     asm volatile("" ::: "memory");
-    load_t(1, t1h, t1l);
-    load_t(2, t2h, t2l);
+    // U(0) is formed here, before any later T - I set goes out. Inside the
+    // loop below, the wait the compiler places in front of a step's products
+    // also covers loads issued after that step's own set. A U(0) formed
+    // there would wait for sets issued after chunk 0 landed (cold T=1141
+    // HV=32 call -0.14 to -0.30 us, bitwise unchanged).
     // step() is false only when a bounded wait gave up
-    for (int c = 0; c < x.nch; c += 3) {
-        if (!step(c, t0h, t0l)) return;
-        if (c + 1 < x.nch && !step(c + 1, t1h, t1l)) return;
-        if (c + 2 < x.nch && !step(c + 2, t2h, t2l)) return;
+    if (!step(0, t0h, t0l, false)) return;
+    load_t(2, t2h, t2l);
+    load_t(3, t0h, t0l);
+    for (int c = 1; c < x.nch; c += 3) {
+        if (!step(c, t1h, t1l)) return;
+        if (c + 1 < x.nch && !step(c + 1, t2h, t2l)) return;
+        if (c + 2 < x.nch && !step(c + 2, t0h, t0l)) return;
     }
 }
 
