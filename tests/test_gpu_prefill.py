@@ -133,6 +133,28 @@ def test_reference_grid_init_state(ops, dev):
     _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="grid init")
 
 
+@pytest.mark.parametrize("B,T,HK,HV,g_shift", [(1, 16384, 2, 4, 2.0), (1, 32768, 1, 2, 4.0),
+                                               (2, 8192, 2, 4, 0.0)])
+def test_long_sequences(ops, dev, B, T, HK, HV, g_shift):
+    """Chains of 128 to 512 chunks, so that error growth over many scan steps
+    (the state carried as an fp32 hi accumulation plus a decayed lo part, the
+    V_n products on its fp16 copy) shows.  The mean gate is -0.81, -0.18 and
+    -0.03 per token for g_shift 0, 2 and 4, so a chunk keeps e^{64 g} ~ 1e-22,
+    8e-6 and 0.15 of the state: with g_shift 4 every step adds to a state
+    that carries far back."""
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(500 + T + HV, B=B, T=T, HK=HK, HV=HV,
+                                              g_shift=g_shift, s0_scale=0.5)
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag=f"long T{T} B{B} HV{HV} g+{g_shift:g}")
+
+
+def test_reference_grid_long(ops, dev):
+    """The reference harness's random distribution (q/k = randn/8, g = -0.3
+    rand, beta = rand; parity_cuda.py:146-153) at S=16384, beyond its grid's
+    longest case (S=3200): 256 chunks, 32 heads."""
+    q, k, v, g, beta, s0 = gc.make_reference_inputs(1, 16384, 16384, l2_pre=True)
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="grid S16384")
+
+
 def test_varlen_edges(ops, dev):
     """Empty, single-token and chunk-boundary lengths in one packed batch."""
     lens = torch.tensor([0, 1, 63, 64, 65, 0, 130, 5])
