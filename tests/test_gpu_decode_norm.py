@@ -35,6 +35,16 @@ def test_multi_token(ops, dev, T, hk, hv):
     _decode_check(ops, dev, q, k, v, g, beta, s0, tag=f"T{T} hk{hk} hv{hv}")
 
 
+@pytest.mark.parametrize("g_shift", [0.0, 4.0])
+def test_multi_token_long(ops, dev, g_shift):
+    """512 tokens in one call (the kernel's token loop keeps the state in
+    registers throughout): no error growth over the steps, with fast and with
+    slow decay."""
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(77 + int(g_shift), B=4, T=512, HK=2, HV=4,
+                                              g_shift=g_shift, s0_scale=0.5)
+    _decode_check(ops, dev, q, k, v, g, beta, s0, tag=f"T512 g+{g_shift:g}")
+
+
 def test_decode_matches_prefill_t1(ops, dev):
     """A T=1 prefill and a decode step compute the same token."""
     q, k, v, g, beta, s0 = [t.to(dev) for t in gc.make_gdn_inputs(9, B=4, T=1, HK=2, HV=4)]
