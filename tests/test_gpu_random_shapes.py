@@ -2,7 +2,8 @@
 length and packed batches, GQA ratios 1/2/4, with and without an initial
 state, so that both scan instances and every chunk-tail case come up), the
 recurrent decode step (batch, tokens per call, GQA ratio, state scale and
-gate range), the causal conv1d prefill (widths with partial channel tiles,
+gate range), the fused raw-input prefill (gate pre-op and in-kernel q/k norm; fp16 and
+bf16 I/O), the causal conv1d prefill (widths with partial channel tiles,
 K = 2..4, both I/O dtypes, bias, both launch regimes), the conv1d decode
 update (the 4-channel vector path and the per-channel path: state lengths
 K-1..8, several tokens per call) and the gated RMSNorm (row counts, head
@@ -22,6 +23,7 @@ import torch
 import gdn_cases as gc
 from oracle import gdn_oracle as orc
 from test_gpu_decode_norm import _decode_check, _norm_check
+from test_gpu_fused import _fused
 
 pytestmark = pytest.mark.gpu
 
@@ -235,3 +237,30 @@ def test_gated_rmsnorm_random_shape(ops, dev, case):
     w = 1 + 0.1 * torch.randn(case["dv"], generator=gen)
     w = w.to(case["io"]) if case["wdt"] == "io" else w
     _norm_check(ops, dev, x, z, w, 1e-6, tag=f"random {shape} w={case['wdt']}")
+
+
+def _fused_cases(n=8, seed=515):
+    gen = torch.Generator().manual_seed(seed)
+
+    def pick(seq):
+        return seq[int(torch.randint(len(seq), (1,), generator=gen))]
+
+    cases = []
+    for i in range(n):
+        hk = pick([1, 2, 4, 8, 16])
+        hv = min(hk * pick([1, 2, 4]), 32)
+        hv -= hv % hk
+        cases.append(dict(seed=600 + i, B=int(torch.randint(1, 4, (1,), generator=gen)),
+                          T=int(torch.randint(2, 600, (1,), generator=gen)), hk=hk, hv=hv,
+                          dtype=pick([torch.float16, torch.bfloat16])))
+    return cases
+
+
+FUSED_CASES = _fused_cases()
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=[f"f{i}" for i in range(len(FUSED_CASES))])
+def test_fused_random_shape(ops, dev, case):
+    _fused(ops, dev, *gc.fused_inputs(case["seed"], B=case["B"], T=case["T"], HK=case["hk"],
+                                      HV=case["hv"], dtype=case["dtype"]),
+           tag=f"random B={case['B']} T={case['T']} HK={case['hk']} HV={case['hv']}")
