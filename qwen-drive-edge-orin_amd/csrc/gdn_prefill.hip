@@ -351,9 +351,14 @@ __device__ bool locate_chunk(const int32_t* cu, int N, int T, int total, int cid
 // it dirty in L2, and the kernel's end must then write back every dirty line
 // before the next kernel may start (the eight XCDs' L2s are not coherent with
 // each other): after the prep's 30 MB of workspace that write-back held the
-// scan back ~5 us, with these stores ~1.3 us.  (Non-temporal stores avoid the
-// write-back too, but the lines then come back from HBM, which slows the
-// scan.)  The prep never waits for these stores.  The scan's o and state
+// scan back ~5 us, with these stores ~1.3 us.  Non-temporal stores (kNt)
+// avoid the write-back too, but the lines then come back from HBM: slower
+// while a call's records fit the 256 MB memory-side cache (T1141 HV32
+// 37.2 -> 40.8 us; up to 233 MB of workspace 3-10 % slower), faster once
+// they do not, when the scan reads them from HBM either way and the written
+// lines only push older ones out (276 to 686 MB of workspace: 3.3-5.5 %
+// faster); the launcher picks them above kNtWorkspaceBytes.  The prep never
+// waits for these stores.  The scan's o and state
 // stores stay plain: a wave's later loads complete only after its earlier
 // stores, and waiting behind write-through stores slowed the output waves by
 // more than the write-back they save.  A store of more than 8 bytes reads its data
@@ -361,21 +366,37 @@ __device__ bool locate_chunk(const int32_t* cu, int N, int T, int total, int cid
 // which the compiler inserts after its own stores but cannot see inside an
 // asm statement, so the 16-byte form carries its own s_nop.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-template <typename V>
+constexpr size_t kNtWorkspaceBytes = size_t(256) << 20;
+template <bool kNt = false, typename V>
 __device__ __forceinline__ void st_through(V* p, const V& v) {
     static_assert(sizeof(V) == 4 || sizeof(V) == 8 || sizeof(V) == 16, "4, 8 or 16 bytes");
     if constexpr (sizeof(V) == 16) {
-        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p),
-                     "v"(__builtin_bit_cast(u32x4, v))
-                     : "memory");
+        if constexpr (kNt)
+            asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(p),
+                         "v"(__builtin_bit_cast(u32x4, v))
+                         : "memory");
+        else
+            asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p),
+                         "v"(__builtin_bit_cast(u32x4, v))
+                         : "memory");
     } else if constexpr (sizeof(V) == 8) {
-        asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p),
-                     "v"(__builtin_bit_cast(u32x2, v))
-                     : "memory");
+        if constexpr (kNt)
+            asm volatile("global_store_dwordx2 %0, %1, off nt" ::"v"(p),
+                         "v"(__builtin_bit_cast(u32x2, v))
+                         : "memory");
+        else
+            asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p),
+                         "v"(__builtin_bit_cast(u32x2, v))
+                         : "memory");
     } else {
-        asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p),
-                     "v"(__builtin_bit_cast(uint32_t, v))
-                     : "memory");
+        if constexpr (kNt)
+            asm volatile("global_store_dword %0, %1, off nt" ::"v"(p),
+                         "v"(__builtin_bit_cast(uint32_t, v))
+                         : "memory");
+        else
+            asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p),
+                         "v"(__builtin_bit_cast(uint32_t, v))
+                         : "memory");
     }
 }
 
@@ -450,7 +471,7 @@ __device__ inline void am_products(const half8 (&ka)[4][4], const half8 (&qf)[4]
     }
 }
 
-template <bool kDbg, int kRaw>
+template <bool kDbg, int kRaw, bool kNt = false>
 __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     PrepIn in, const int32_t* __restrict__ cu, int N, int T, int total, int HV, int HK,
     int nch_bound, float scale, Workspace ws) {
@@ -607,7 +628,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         if (writer) {
             half8* qdst = ws.Q + ((size_t)cid * HK + hk) * 16 * 64;
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) st_through(&qdst[(wave * 4 + kb) * 64 + lane], qf[kb]);
+            for (int kb = 0; kb < 4; ++kb) st_through<kNt>(&qdst[(wave * 4 + kb) * 64 + lane], qf[kb]);
         }
     }
 
@@ -628,10 +649,10 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
         sm.b[lane] = bv;
         sm.bec[lane] = bv * ec;
         float* gr = ws.gates + ch * (kGateBytes / 4);
-        st_through(&gr[kGBeta + lane], bv);
-        st_through(&gr[kGDec + lane], lane < rows ? __builtin_amdgcn_exp2f((c63 - cs) * kLog2e) : 0.f);
-        st_through(&gr[kGSec + lane], scale * ec);
-        st_through(&gr[kGC63 + lane], lane == 0 ? c63 : 0.f);
+        st_through<kNt>(&gr[kGBeta + lane], bv);
+        st_through<kNt>(&gr[kGDec + lane], lane < rows ? __builtin_amdgcn_exp2f((c63 - cs) * kLog2e) : 0.f);
+        st_through<kNt>(&gr[kGSec + lane], scale * ec);
+        st_through<kNt>(&gr[kGC63 + lane], lane == 0 ? c63 : 0.f);
         if (kDbg) ws.dbgC[ch * kChunk + lane] = cs;
     }
     asm volatile("" ::"v"(ts0));   // the share is read (and waited for) before the products
@@ -691,8 +712,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             mh[mt] = to_half4(val);
         }
         half8* mdst = ws.M + ch * (kTri * 64);
-        st_through(&mdst[tri_base(wave) * 64 + lane], cat8(mh[0], mh[1]));
-        if (wave >= 2) st_through(&mdst[(tri_base(wave) + 1) * 64 + lane], cat8(mh[2], mh[3]));
+        st_through<kNt>(&mdst[tri_base(wave) * 64 + lane], cat8(mh[0], mh[1]));
+        if (wave >= 2) st_through<kNt>(&mdst[(tri_base(wave) + 1) * 64 + lane], cat8(mh[2], mh[3]));
     }
     __syncthreads();
 
@@ -804,8 +825,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
             }
             half8 hi, lo;
             split_hilo8(t0, t1, hi, lo);
-            st_through(&tdst[(tri_base(mt) + kb) * 64 + lane], hi);
-            st_through(&ldst[(tri_base(mt) + kb) * 64 + lane], lo);
+            st_through<kNt>(&tdst[(tri_base(mt) + kb) * 64 + lane], hi);
+            st_through<kNt>(&ldst[(tri_base(mt) + kb) * 64 + lane], lo);
         }
     }
 
@@ -832,7 +853,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                     bf16x8 kb16;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) kb16[e] = (__bf16)(float)kt[tt][kb][e];
-                    st_through(&ktdst[((2 * wave + tt) * 2 + kb) * 64 + lane],
+                    st_through<kNt>(&ktdst[((2 * wave + tt) * 2 + kb) * 64 + lane],
                                __builtin_bit_cast(u32x4, kb16));
                 }
             }
@@ -858,7 +879,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                 acc0 = mfma16(kt[0][kb], bt, acc0);
                 acc1 = mfma16(kt[1][kb], bt, acc1);
             }
-            st_through(&wdst[(mt * 4 + wave) * 64 + lane], cat8(to_half4(-acc0), to_half4(-acc1)));
+            st_through<kNt>(&wdst[(mt * 4 + wave) * 64 + lane], cat8(to_half4(-acc0), to_half4(-acc1)));
         }
     }
 }
@@ -2526,9 +2547,13 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
         const int rep = HV / HK;
         const size_t groups = (nch_bound * (size_t)HK + 7) / 8;
         const size_t grid = std::max<size_t>(groups * 8 * rep, 1);
-        auto kern = raw == 1 ? gdn_prep_kernel<false, 1>
-                    : raw == 2 ? gdn_prep_kernel<false, 2>
-                    : dump_debug ? gdn_prep_kernel<true, 0> : gdn_prep_kernel<false, 0>;
+        // records that cannot stay in the memory-side cache go out
+        // non-temporally (see st_through)
+        const bool nt = !dump_debug && need > kNtWorkspaceBytes;
+        auto kern = raw == 1 ? (nt ? gdn_prep_kernel<false, 1, true> : gdn_prep_kernel<false, 1>)
+                    : raw == 2 ? (nt ? gdn_prep_kernel<false, 2, true> : gdn_prep_kernel<false, 2>)
+                    : dump_debug ? gdn_prep_kernel<true, 0>
+                    : nt ? gdn_prep_kernel<false, 0, true> : gdn_prep_kernel<false, 0>;
         PrepIn pin = in;
         pin.s0 = s0;
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kPrepThreads), 0, stream, pin, cu, N, T,

@@ -147,6 +147,14 @@ def test_long_sequences(ops, dev, B, T, HK, HV, g_shift):
     _run_and_check(ops, dev, q, k, v, g, beta, s0, tag=f"long T{T} B{B} HV{HV} g+{g_shift:g}")
 
 
+def test_workspace_beyond_the_memory_side_cache(ops, dev):
+    """B2 T4096 HV32 HK16: 276 MB of workspace, more than the 256 MB
+    memory-side cache, so the prep writes its records non-temporally; 512
+    16-column groups, so the paired scan runs."""
+    q, k, v, g, beta, s0 = gc.make_gdn_inputs(4096, B=2, T=4096, HK=16, HV=32, g_shift=2.0)
+    _run_and_check(ops, dev, q, k, v, g, beta, s0, tag="T4096 B2 HV32 (276 MB workspace)")
+
+
 def test_reference_grid_long(ops, dev):
     """The reference harness's random distribution (q/k = randn/8, g = -0.3
     rand, beta = rand; parity_cuda.py:146-153) at S=16384, beyond its grid's
