@@ -604,7 +604,7 @@ def trace_from_profiles():
     if not p.exists():
         return {}
     out = {}
-    for m in re.finditer(r"^\| (gdn_prep_kernel<false,0>|gdn_scan_kernel<0,false,false>) \| \d+ \| "
+    for m in re.finditer(r"^\| (gdn_prep_kernel<false,0,false>|gdn_scan_kernel<0,false,false>) \| \d+ \| "
                          r"([0-9.]+) \|.*\| (\d+)x1 \| \d+ \|$", p.read_text(), flags=re.M):
         name = m.group(1).split("<")[0]
         grid = int(m.group(3))
