@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product path imports this module:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` use it, and only as the checker (or the timed CPU baseline).
+``bench.py`` use it, and only as the reference that results are compared with
+(or as the timed CPU baseline).
 
 It restates, in plain torch CPU code (fp32 or fp64), the algorithm the
 reference's kernels are gated against.  The defining code is the third-party

@@ -15,7 +15,7 @@ tensors can be moved to the GPU and handed to the oracle):
 
 Metrics restate kernels/harness/parity_test.py:124-153 (row_cos_min,
 max_rel with denominator floor 0.1, tensor_l2_rel) plus max/mean absolute
-error, the bar this build is held to (max |err| <= 2e-2 on o and state).
+error, the bar these kernels are held to (max |err| <= 2e-2 on o and state).
 """
 from __future__ import annotations
 

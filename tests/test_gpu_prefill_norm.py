@@ -78,7 +78,7 @@ def test_prefill_norm_fused_matches_two_steps(ops, dev, B, T, HK, HV):
 
 def test_prefill_norm_matches_oracle(ops, dev):
     """The fused path; two pins.  (1) The epilogue: y against the oracle's
-    gated RMSNorm applied to this build's own o (chunk_prefill's output, the
+    gated RMSNorm applied to the library's own o (chunk_prefill's output, the
     same bits the fused scan normalises), to the bar of the two-step test.  (2) End to end
     against the fp64 oracle: y = gated_rmsnorm(o) scales o's absolute error by
     |w silu(z)| / rms(o), so the bar is the reference harness's fixture bar on
