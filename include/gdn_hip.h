@@ -146,17 +146,15 @@ hipError_t deltanet_chunk_prefill_norm(const void* q, const void* k, const void*
                                        void* workspace, size_t workspace_bytes,
                                        hipStream_t stream);
 
-/* deltanet_chunk_prefill_norm with the gated RMSNorm fused into the scan's
- * output stage, so o is never stored (no counterpart in the reference).  The
- * 8 work-groups that share a row's 128 columns wait on each other's sums of
- * squares, so the scan is launched cooperatively -- the runtime starts it only
- * with every group resident -- when the runtime's occupancy figure says the
- * grid (8 * B * HV groups, rounded up to 64) fits the device at once;
- * otherwise this runs deltanet_chunk_prefill_norm's two kernels.  A wait that
- * still gives up (bounded, ~0.1 s) leaves y incomplete and sets the status
- * word deltanet_prefill_status reports.  Same arguments and results as
- * deltanet_chunk_prefill_norm; a row's rsqrt may differ from it in the last
- * bit (the row sum is associated differently). */
+/* deltanet_chunk_prefill_norm with the gated RMSNorm inside the scan (no
+ * counterpart in the reference): each of the 8 work-groups that share a row's
+ * 128 columns writes its o columns of a chunk and counts itself in with a
+ * device-scope atomic; the group that completes the count normalises that
+ * chunk of the head in place, with the standalone kernel's arithmetic.  No
+ * group waits on another.  Where the plain prefill would take the paired
+ * 32-column scan (more slice groups than CUs) this runs
+ * deltanet_chunk_prefill_norm's two kernels.  Same arguments and the same
+ * bits as deltanet_chunk_prefill_norm; slower than it (opt-in). */
 hipError_t deltanet_chunk_prefill_norm_fused(const void* q, const void* k, const void* v,
                                              const float* g, const float* beta, const void* z,
                                              const void* norm_weight, float eps, void* y,

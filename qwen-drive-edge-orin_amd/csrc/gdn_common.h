@@ -97,4 +97,27 @@ __device__ __forceinline__ f32x4 zero4() {
     return z;
 }
 
+// x + (x of the lane the DPP control names), every lane's source valid
+template <int kCtrl>
+__device__ __forceinline__ float dpp_sum(float x) {
+    const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, true);
+    return x + __builtin_bit_cast(float, t);
+}
+
+// Sum over each aligned group of N lanes (N a power of two), the same value
+// in every lane of the group, added in the order of an xor butterfly (lane
+// i with i ^ 1, then i ^ 2, ...): within 16 lanes by DPP moves (quad
+// permutes, then the half-row and row mirrors, which pair the same sums),
+// across rows by LDS permutes.
+template <int N>
+__device__ inline float lane_group_sum(float x) {
+    if constexpr (N > 1) x = dpp_sum<0xB1>(x);    // quad_perm [1,0,3,2]
+    if constexpr (N > 2) x = dpp_sum<0x4E>(x);    // quad_perm [2,3,0,1]
+    if constexpr (N > 4) x = dpp_sum<0x141>(x);   // row_half_mirror
+    if constexpr (N > 8) x = dpp_sum<0x140>(x);   // row_mirror
+#pragma unroll
+    for (int m = 16; m < N; m <<= 1) x += __shfl_xor(x, m, 64);
+    return x;
+}
+
 }  // namespace gdn

@@ -92,7 +92,7 @@ constexpr size_t kWBytes = 16 * kFrag;                 // 16 KB
 constexpr size_t kGateBytes = 1024;
 constexpr size_t kQBytes = 16 * kFrag;                 // 16 KB
 constexpr size_t kKTBytes = 16 * kFrag;                // 16 KB
-constexpr size_t kSsqBytes = (size_t)kSlices * kChunk * 4;   // 2 KB
+constexpr size_t kNormCntBytes = 16;   // one arrival counter per chunk-head (16-byte store)
 constexpr size_t kHeaderBytes = 256;
 
 // gates record: float offsets
@@ -106,7 +106,7 @@ struct Workspace {
     float* gates;       // [chunk-head][256]
     half8* Q;           // Q fragments [chunk * HK + hk][mt * 4 + kb][64]
     u32x4* KT;          // K^T bf16 fragments [chunk * HK + hk][t * 2 + kb][64]
-    uint32_t* ssq;      // [chunk-head][slice][64] fp32 bits, sign bit set = not yet written (null outside the norm epilogue)
+    uint32_t* ncnt;     // [chunk-head][4]: word 0 counts the slice groups whose o is written (norm epilogue only, else null)
     unsigned* status;   // bit 0: a bounded wait gave up
     float* dbgT;        // optional [chunk-head][64][64]: T = (I - A)^-1
     float* dbgA;        // optional: A
@@ -121,7 +121,7 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 // Byte layout of the workspace for `nch` chunk-heads.  The debug regions stay
 // last: the torch binding finds them from the end.
 struct WsLayout {
-    size_t ti, tilo, m, w, gates, q, kt, ssq, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
+    size_t ti, tilo, m, w, gates, q, kt, ncnt, dbgT, dbgA, dbgTp, dbgM, dbgC, dbgS, live, total;
     __host__ explicit WsLayout(size_t nch) {
         size_t off = kHeaderBytes;
         ti = off;    off += align256(nch * kTriBytes);
@@ -131,7 +131,7 @@ struct WsLayout {
         gates = off; off += align256(nch * kGateBytes);
         q = off;     off += align256(nch * kQBytes);
         kt = off;    off += align256(nch * kKTBytes);
-        ssq = off;   off += align256(nch * kSsqBytes);
+        ncnt = off;  off += align256(nch * kNormCntBytes);
         live = off;
         dbgT = off;  off += align256(nch * kChunk * kChunk * 4);
         dbgA = off;  off += align256(nch * kChunk * kChunk * 4);
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
     // use waits before the branch that leads to the next): fields at most 32
     // bytes apart, all requested together, cost one.
     asm volatile("" ::"s"(in.q), "s"(in.A_log), "s"(cu), "s"(nch_bound), "s"(ws.TIlo),
-                 "s"(ws.gates), "s"(ws.ssq), "s"(ws.dbgT), "s"(ws.dbgM), "s"(ws.dbgS));
+                 "s"(ws.gates), "s"(ws.ncnt), "s"(ws.dbgT), "s"(ws.dbgM), "s"(ws.dbgS));
     const uint16_t* __restrict__ q = in.q;
     const uint16_t* __restrict__ k = in.k;
     const int tid = threadIdx.x;
@@ -508,11 +508,11 @@ __global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(
                                     tok0, rows))
         return;
     const size_t ch = (size_t)cid * HV + hv;
-    // this call's gated-RMSNorm slots start invalid (2 KB: 16 bytes a
-    // thread; only when the scan runs the norm epilogue)
-    if (ws.ssq && tid < kSlices * kChunk / 4)
-        st_through(reinterpret_cast<u32x4*>(ws.ssq + ch * (kSlices * kChunk)) + tid,
-                   u32x4{~0u, ~0u, ~0u, ~0u});
+    // this call's gated-RMSNorm arrival counter of the chunk-head starts at
+    // zero (only when the scan runs the norm epilogue)
+    if (ws.ncnt && tid == 0)
+        st_through(reinterpret_cast<u32x4*>(ws.ncnt + ch * (kNormCntBytes / 4)),
+                   u32x4{0u, 0u, 0u, 0u});
 
     // ---- global loads, all issued before any is consumed.  Rows past the
     // chunk's end read the last valid row and are zeroed afterwards.
@@ -966,14 +966,9 @@ struct ScanSmem {
     int abort;       // a bounded wait ran out: every wave stops
     int seqsel;
     int red[kScanWaves];
-    // norm epilogue, per output wave: a chunk's sums of squares per (tile,
-    // token, lane group), then per token the sum over the 8 slices
-    float npart[2][4][16][4];
-    float ntot[2][64];
-    int npub[2];     // per output wave: chunks whose partial sums are in npart
-    int nfree[2];    // per output wave: chunks whose npart the norm wave has read
-    int ntok[2];     // per output wave: chunks whose row totals are in ntot
-    int nread[2];    // per output wave: chunks whose ntot it has read
+    // norm epilogue, per output wave: chunks of its parity whose o is written
+    // (stores complete at the device-coherent level)
+    int npub[2];
 };
 
 __device__ __forceinline__ int lds_ld(const int* p) {
@@ -1524,68 +1519,118 @@ __device__ void run_lo_helper(ScanSmem& sm, const ScanArgs& a, const Waiter& w, 
 }
 
 // Gated-RMSNorm epilogue (kNorm; bf16 o, z and weight), y = gated_rmsnorm(o, z)
-// with the transformers rounding steps (modeling_qwen3_5.py:175-184):
-// n = bf16(o * rsqrt(mean(o^2) + eps)), h = bf16(w * n), y = bf16(h * silu(z)),
-// o being the bf16 value the plain prefill would store.  A row's 128 columns
-// are spread over the 8 slice groups of its head, so each group publishes its
-// 16-column sum of squares per token in a 32-bit slot (device-scope atomic
-// store of the fp32 bits, sign bit clear; the prep fills every slot with
-// all-ones first, and each slot is written once per call, so a reader needs
-// no ordering between slots) and sums the 8 slots in slice order, the same
-// sum in every group.  A chunk is finished one chunk of the wave later, when
-// the other groups' slots are normally in.
-__device__ inline uint32_t* ssq_slots(const ScanArgs& a, const ScanCtx& x, int c) {
-    return a.ws.ssq + ((size_t)(x.chunk0 + c) * a.HV + x.hv) * (kSlices * kChunk);
+// in place over o, with the arithmetic of gated_rmsnorm_kernel (bf16, 8
+// lanes per row of 128, two 16-byte pieces a lane: the same sums in the same
+// order, so the same bits as the prefill followed by that kernel).  A row's
+// 128 columns come from the 8 slice groups of its head.  Each output wave
+// writes its chunk's o through to the device-coherent level and waits for
+// those stores; the norm wave (wave 4) then adds 1 to the chunk-head's
+// arrival counter (device-scope atomic; the prep zeroes it).  The group that
+// brings it to 8 normalises the whole chunk-head, reading the other groups'
+// o with device-scope loads.  No group waits on another.
+__device__ inline uint32_t* norm_counter(const ScanArgs& a, const ScanCtx& x, int c) {
+    return a.ws.ncnt + ((size_t)(x.chunk0 + c) * a.HV + x.hv) * (kNormCntBytes / 4);
 }
 
-// Norm wave (wave 4, norm epilogue only): the device-scope traffic of the
-// row sums, kept off the output waves, whose loads would otherwise wait behind
-// each device-scope store.  Per chunk c, in order: token L's sum over this
-// slice's 16 columns (lane groups in order) from npart into its slot; then
-// chunk c - 1's 8 slots of each token, polled until valid and summed in
-// slice order, into ntot for the output wave of c - 1.
+// 16 bytes of o written by any group of the call: two device-scope 8-byte loads
+__device__ __forceinline__ u32x4 ld_o_agent(const uint16_t* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+
+// y for chunk c of this (sequence, v-head), all 128 columns: lane = 8 rr +
+// sub takes rows rr, rr + 8, ... and columns 8 sub .. + 7 and 64 + 8 sub .. + 7
+__device__ void norm_chunk(const ScanArgs& a, const ScanCtx& x, int c, const u32x4 (&wr)[2],
+                           int lane) {
+    constexpr int kPasses = kChunk / 8;
+    const int sub = lane & 7, rr = lane >> 3;
+    const int rows = min(kChunk, x.len - c * kChunk);
+    u32x4 xr[kPasses][2], zr[kPasses][2];
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+        const int r = min(8 * ps + rr, rows - 1);
+        const size_t off = ((size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv) * kDV + 8 * sub;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            xr[ps][j] = ld_o_agent(a.o + off + 64 * j);
+            zr[ps][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.z + off + 64 * j));
+        }
+    }
+    float wf[2][8];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            wf[j][2 * q] = bf16_bits_to_f32(wr[j][q] & 0xffffu);
+            wf[j][2 * q + 1] = bf16_bits_to_f32(wr[j][q] >> 16);
+        }
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+        float xf[2][8], zf[2][8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xf[j][2 * q] = bf16_bits_to_f32(xr[ps][j][q] & 0xffffu);
+                xf[j][2 * q + 1] = bf16_bits_to_f32(xr[ps][j][q] >> 16);
+                zf[j][2 * q] = bf16_bits_to_f32(zr[ps][j][q] & 0xffffu);
+                zf[j][2 * q + 1] = bf16_bits_to_f32(zr[ps][j][q] >> 16);
+            }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(xf[j][e], xf[j][e], ss);
+        ss = lane_group_sum<8>(ss);
+        const float rs = 1.0f / sqrtf(ss / (float)kDV + a.eps);
+        u32x4 y4[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int e = 2 * q + h;
+                    const float n = bf16_bits_to_f32(f32_to_bf16_bits(xf[j][e] * rs));
+                    const float hv = bf16_bits_to_f32(f32_to_bf16_bits(wf[j][e] * n));
+                    const float sz = zf[j][e] * __builtin_amdgcn_rcpf(
+                                                    1.0f + __builtin_amdgcn_exp2f(zf[j][e] * -1.44269504088896341f));
+                    pk |= (uint32_t)f32_to_bf16_bits(hv * sz) << (16 * h);
+                }
+                y4[j][q] = pk;
+            }
+        if (8 * ps + rr < rows) {
+            const size_t off =
+                ((size_t)(x.tok_base + c * kChunk + 8 * ps + rr) * a.HV + x.hv) * kDV + 8 * sub;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                __builtin_nontemporal_store(y4[j], reinterpret_cast<u32x4*>(a.o + off + 64 * j));
+        }
+    }
+}
+
+// Norm wave (wave 4, norm epilogue only): per chunk, once this group's o for
+// it is written, count the group in; the eighth group normalises the chunk.
 __device__ void run_norm(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                          int lane) {
-    auto totals = [&](int cg) -> bool {
-        const int jg = cg & 1, kg = cg >> 1;
-        const uint32_t* slots = ssq_slots(a, x, cg);
-        uint32_t v[kSlices];
-        auto poll = [&] {
-            bool ok = true;
+    u32x4 wr[2];
 #pragma unroll
-            for (int sl = 0; sl < kSlices; ++sl) {
-                v[sl] = __hip_atomic_load(slots + sl * kChunk + lane, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-                ok = ok && (v[sl] >> 31) == 0;
-            }
-            return __all(ok) != 0;
-        };
-        if (!w.until(poll)) return false;
-        float tot = 0.f;
-#pragma unroll
-        for (int sl = 0; sl < kSlices; ++sl) tot += __uint_as_float(v[sl]);
-        // ntot[jg] held chunk cg - 2's totals until its output wave read them
-        if (!w.until([&] { return lds_ld(&sm.nread[jg]) >= kg; })) return false;
-        asm volatile("" ::: "memory");
-        sm.ntot[jg][lane] = tot;
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.ntok[jg], kg + 1);
-        return true;
-    };
+    for (int j = 0; j < 2; ++j)
+        wr[j] = *reinterpret_cast<const u32x4*>(a.nw + 8 * (lane & 7) + 64 * j);
     for (int c = 0; c < x.nch; ++c) {
         const int jc = c & 1, kc = c >> 1;
         if (!w.until([&] { return lds_ld(&sm.npub[jc]) >= kc + 1; })) return;
         asm volatile("" ::: "memory");
-        const f32x4 pp = *reinterpret_cast<const f32x4*>(&sm.npart[jc][lane >> 4][lane & 15][0]);
-        const float ssl = ((pp[0] + pp[1]) + pp[2]) + pp[3];
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.nfree[jc], kc + 1);
-        __hip_atomic_store(ssq_slots(a, x, c) + x.sl * kChunk + lane,
-                           __float_as_uint(ssl) & 0x7fffffffu, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        if (c > 0 && !totals(c - 1)) return;
+        unsigned old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(norm_counter(a, x, c), 1u, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 0, 64);
+        if (old == kSlices - 1) norm_chunk(a, x, c, wr, lane);
     }
-    if (x.nch > 0) (void)totals(x.nch - 1);
 }
 
 // Output wave j (0 or 1): chunks j, j + 2, ...
@@ -1593,79 +1638,6 @@ template <int kRaw, bool kNorm>
 __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, const ScanCtx& x,
                            int j, int lane) {
     const int lg = lane >> 4, lm = lane & 15;
-    // norm epilogue: this lane's weights (columns 4 lg .. + 3 of the slice)
-    // and the wave's previous chunk, held until it is finished
-    float wn[4] = {0.f, 0.f, 0.f, 0.f};
-    uint2 xprev[4];
-    int cprev = -1;
-    if constexpr (kNorm) {
-        const uint2 wr = *reinterpret_cast<const uint2*>(a.nw + kSliceCols * x.sl + 4 * lg);
-        wn[0] = bf16_bits_to_f32(wr.x & 0xffffu);
-        wn[1] = bf16_bits_to_f32(wr.x >> 16);
-        wn[2] = bf16_bits_to_f32(wr.y & 0xffffu);
-        wn[3] = bf16_bits_to_f32(wr.y >> 16);
-    }
-    // y for chunk cf from its o values xo: gather() issues the loads of cf's
-    // z, so they land while the wave waits for and computes its next chunk;
-    // finish() takes the rows' sums of squares over all 128 columns from the
-    // norm wave (through ntot) and stores y.
-    struct Gather {
-        uint2 z[4];
-    };
-    auto gather = [&](int cf, Gather& gt) {
-        const int rows = min(kChunk, x.len - cf * kChunk);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const int r = min(16 * mt + lm, rows - 1);
-            gt.z[mt] = *reinterpret_cast<const uint2*>(
-                a.z + ((size_t)(x.tok_base + cf * kChunk + r) * a.HV + x.hv) * kDV +
-                kSliceCols * x.sl + 4 * lg);
-        }
-    };
-    auto finish = [&](int cf, const uint2 (&xo)[4], Gather& gt) -> bool {
-        const int rows = min(kChunk, x.len - cf * kChunk);
-        const int kf = cf >> 1;
-        if (!w.until([&] { return lds_ld(&sm.ntok[j]) >= kf + 1; })) return false;
-        asm volatile("" ::: "memory");
-        float tsum[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) tsum[mt] = sm.ntot[j][16 * mt + lm];
-        lds_wait_all();
-        if (lane == 0) lds_st(&sm.nread[j], kf + 1);
-
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const float ss = tsum[mt];
-            const float rs = 1.0f / sqrtf(ss / (float)kDV + a.eps);
-            const uint32_t xw[2] = {xo[mt].x, xo[mt].y};
-            const uint32_t zw[2] = {gt.z[mt].x, gt.z[mt].y};
-            uint32_t out[2];
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                uint32_t pk = 0;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const float xv = bf16_bits_to_f32(h ? xw[p] >> 16 : xw[p] & 0xffffu);
-                    const float zv = bf16_bits_to_f32(h ? zw[p] >> 16 : zw[p] & 0xffffu);
-                    const float n = bf16_bits_to_f32(f32_to_bf16_bits(xv * rs));
-                    const float hv = bf16_bits_to_f32(f32_to_bf16_bits(wn[2 * p + h] * n));
-                    const float sz = zv * __builtin_amdgcn_rcpf(
-                                              1.0f + __builtin_amdgcn_exp2f(zv * -1.44269504088896341f));
-                    pk |= (uint32_t)f32_to_bf16_bits(hv * sz) << (16 * h);
-                }
-                out[p] = pk;
-            }
-            const int r = 16 * mt + lm;
-            if (r < rows) {
-                uint2* dst = reinterpret_cast<uint2*>(
-                    a.o + ((size_t)(x.tok_base + cf * kChunk + r) * a.HV + x.hv) * kDV +
-                    kSliceCols * x.sl + 4 * lg);
-                *dst = make_uint2(out[0], out[1]);
-            }
-        }
-        return true;
-    };
-    Gather gt;
     // Q and M fragments and s e^c go straight to registers; the next chunk's
     // loads are issued as soon as the current chunk's products have read them
     half8 qf[16], mf[kTri];
@@ -1691,9 +1663,6 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
     load(j);
     for (int c = j; c < x.nch; c += 2) {
         const int hs = c % kHand;
-        if constexpr (kNorm) {
-            if (cprev >= 0) gather(cprev, gt);
-        }
         if (!w.until([&] { return lds_ld(&sm.ready) >= c + 1; })) return;
         asm volatile("" ::: "memory");
         half8 hsf[4], hvf[2];
@@ -1720,10 +1689,10 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
             if (mt >= 2) ov[mt] = mfma16(hvf[1], mf[tri_base(mt) + 1], ov[mt]);
         }
         // the products have read Q, M and s e^c: the next chunk's go out now
+        // (norm epilogue: after this chunk's o stores, which are waited for)
         asm volatile("" : "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));
-        load(c + 2);
+        if constexpr (!kNorm) load(c + 2);
         const int rows = min(kChunk, x.len - c * kChunk);
-        uint2 xnew[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const int r = 16 * mt + lm;
@@ -1736,41 +1705,20 @@ __device__ void run_output(ScanSmem& sm, const ScanArgs& a, const Waiter& w, con
             }
             pk.x = b[0] | (b[1] << 16);
             pk.y = b[2] | (b[3] << 16);
-            if constexpr (kNorm) {
-                // this lane's 4 columns of token r: sum of squares of the
-                // bf16 values, to LDS for the per-token sum below
-                float ssp = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float xv = bf16_bits_to_f32(b[e]);
-                    ssp = fmaf(xv, xv, ssp);
-                }
-                if (mt == 0 && !w.until([&] { return lds_ld(&sm.nfree[j]) >= (c >> 1); }))
-                    return;
-                sm.npart[j][mt][lm][lg] = ssp;
-                xnew[mt] = pk;
-            } else if (r < rows) {
+            if (r < rows) {
                 uint2* dst = reinterpret_cast<uint2*>(
                     a.o + ((size_t)(x.tok_base + c * kChunk + r) * a.HV + x.hv) * kDV +
                     kSliceCols * x.sl + 4 * lg);
-                *dst = pk;
+                if constexpr (kNorm) st_through(dst, pk);   // read back by another group
+                else *dst = pk;
             }
         }
         if constexpr (kNorm) {
-            // this chunk's partial sums to the norm wave
-            lds_wait_all();
+            // the stores have reached the device-coherent level: the norm
+            // wave may count this group in for the chunk
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             if (lane == 0) lds_st(&sm.npub[j], (c >> 1) + 1);
-            // the wave's previous chunk: the other groups' sums are in by now
-            if (cprev >= 0 && !finish(cprev, xprev, gt)) return;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) xprev[mt] = xnew[mt];
-            cprev = c;
-        }
-    }
-    if constexpr (kNorm) {
-        if (cprev >= 0) {
-            gather(cprev, gt);
-            (void)finish(cprev, xprev, gt);
+            load(c + 2);
         }
     }
 }
@@ -1855,12 +1803,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_scan_kernel(ScanArgs a) {
         lds_st(&sm.scdone, 0);
         lds_st(&sm.npub[0], 0);
         lds_st(&sm.npub[1], 0);
-        lds_st(&sm.nfree[0], 0);
-        lds_st(&sm.nfree[1], 0);
-        lds_st(&sm.ntok[0], 0);
-        lds_st(&sm.ntok[1], 0);
-        lds_st(&sm.nread[0], 0);
-        lds_st(&sm.nread[1], 0);
         lds_st(&sm.abort, 0);
     }
     __syncthreads();
@@ -2506,9 +2448,6 @@ bool use_pair_scan(int cols, int N, int HV, int dump_debug, bool norm) {
     return (long long)N * HV * kSlicesPerHead > device_cus();
 }
 
-// The norm epilogue's work-groups wait on each other, so its scan is launched
-// cooperatively (all groups resident at once, or no launch at all); norm !=
-// nullptr requires it.
 hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, float* sf,
                           const int32_t* cu, int N, int T, int total_tokens, int HV, int HK,
                           size_t nch_bound, void* workspace, size_t workspace_bytes,
@@ -2529,7 +2468,7 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     ws.gates = reinterpret_cast<float*>(base + L.gates);
     ws.Q = reinterpret_cast<half8*>(base + L.q);
     ws.KT = reinterpret_cast<u32x4*>(base + L.kt);
-    ws.ssq = norm ? reinterpret_cast<uint32_t*>(base + L.ssq) : nullptr;   // norm epilogue only
+    ws.ncnt = norm ? reinterpret_cast<uint32_t*>(base + L.ncnt) : nullptr;   // norm epilogue only
     ws.status = reinterpret_cast<unsigned*>(base);
     if (dump_debug) {
         ws.dbgT = reinterpret_cast<float*>(base + L.dbgT);
@@ -2589,9 +2528,9 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
         hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), 0, stream, sa);
         err = hipGetLastError();
     } else if (norm) {
-        void* kargs[] = {&sa};
-        err = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(gdn_scan_kernel<0, false, true>),
-                                         dim3(grid), dim3(kScanThreads), kargs, 0, stream);
+        hipLaunchKernelGGL((gdn_scan_kernel<0, false, true>), dim3(grid), dim3(kScanThreads), 0,
+                           stream, sa);
+        err = hipGetLastError();
     } else {
         auto scan = raw == 1 ? gdn_scan_kernel<1, false>
                     : raw == 2 ? gdn_scan_kernel<2, false>
@@ -2601,24 +2540,6 @@ hipError_t launch_prefill(const PrepIn& in, int raw, void* o, const float* s0, f
     }
     if (ev) (void)hipEventRecord(ev[2], stream);
     return err;
-}
-
-// Whether `groups` work-groups of the norm epilogue's scan fit on the current
-// device at once (the occupancy the runtime reports for that kernel), and the
-// device supports cooperative launches.
-bool norm_scan_coresident(long long groups) {
-    int dev = 0, coop = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
-        !coop)
-        return false;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return false;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(gdn_scan_kernel<0, false, true>), kScanThreads,
-            0) != hipSuccess)
-        return false;
-    return groups <= (long long)per_cu * cus;
 }
 
 constexpr int kPrefillKernels = 2;
@@ -2724,12 +2645,10 @@ extern "C" hipError_t deltanet_chunk_prefill_norm_fused(
     if (!norm_args_ok(q, k, v, g, beta, z, norm_weight, eps, y, final_state, B, T, HV, HQK, DK,
                       DV, chunk_size, workspace))
         return hipErrorInvalidValue;
-    // The epilogue's groups wait on each other (the 8 slice groups of a head
-    // share every row's sum of squares): it runs only when the runtime's
-    // occupancy figure says the whole scan grid fits at once, and then as a
-    // cooperative launch, which the runtime starts only with every group
-    // resident.  Otherwise the two-kernel path runs.
-    if (!norm_scan_coresident(scan_groups(B, HV)))
+    // The epilogue lives in the 16-column scan; where the plain prefill would
+    // take the paired 32-column instance (more slice groups than CUs) the
+    // two-kernel path runs instead.
+    if (use_pair_scan(0, B, HV, 0, false))
         return prefill_then_norm(q, k, v, g, beta, z, norm_weight, eps, y, initial_state,
                                  final_state, B, T, HV, HQK, workspace, workspace_bytes, stream);
     const size_t nc = (size_t)B * ((T + kChunk - 1) / kChunk);

@@ -202,8 +202,8 @@ std::vector<at::Tensor> chunk_prefill_debug(at::Tensor q, at::Tensor k, at::Tens
 
 // Prefill followed by the gated RMSNorm: returns [y, final_state], y =
 // gated_rmsnorm(o, z, weight, eps) for the o that chunk_prefill would return
-// (bf16 o, z and weight).  fused=True runs the RMSNorm in the scan's output
-// stage (deltanet_chunk_prefill_norm_fused), so o is never stored.
+// (bf16 o, z and weight).  fused=True runs the RMSNorm inside the scan
+// (deltanet_chunk_prefill_norm_fused; the same bits).
 std::vector<at::Tensor> chunk_prefill_norm(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor g,
                                            at::Tensor beta, at::Tensor z, at::Tensor weight,
                                            std::optional<at::Tensor> s0, double eps,
